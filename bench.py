@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 quantized-linear hot path on one MI355X.
+
+Headline (BASELINE.json `metric`, configs[1]): decode dequant-GEMV, W int8
+[4096, 4096] with per-row f32 scales, X fp16 [1, 4096], Y fp16.  One step is
+one GEMV over one weight copy; 48 distinct copies (806 MB, > 2x the 256 MB
+Infinity Cache) rotate so every step reads its weight from HBM.  Steps are
+replayed from a HIP graph of 48 launches (remainder launched directly), all
+on the context's stream.
+
+Printed JSON (one line, stdout):
+  value            whole-job GB/s = algorithmic bytes x steps / timed wall time
+  roofline         dominant kernel (the GEMV): algorithmic bytes / mean kernel
+                   duration from per-launch HIP event pairs, vs 8 TB/s
+  cpu_baseline     the reference's per-token path on host cores: k-ascending
+                   f32 GEMV on the load-time-dequantized f32 weight (oracle port)
+  prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
+  decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2])
+
+Algorithmic bytes per GEMV = N*K (codes) + 4*N (scales) + 2*M*K (X) + 2*M*N (Y).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+COPIES = 48
+METRIC = "int8 GEMV GB/s (% HBM peak) at 4096² M=1; prefill TFLOPS; decode tok/s"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemv_bytes(m: int, n: int, k: int) -> int:
+    return n * k + 4 * n + 2 * m * k + 2 * m * n
+
+
+class GemvWorkload:
+    """COPIES rotating per-row int8 weights [n, k] plus X [m, k], Y [m, n] fp16."""
+
+    def __init__(self, ctx, m: int, n: int, k: int, seed: int = 0, copies: int = COPIES):
+        from rusty_amd import DType, UnifiedTensor, _lib, synth
+
+        self.ctx, self.m, self.n, self.k, self.copies = ctx, m, n, k, copies
+        g = synth.rng(seed)
+        q, s = synth.rowwise_weight(g, n, k)
+        x = synth.activations(g, m, k)
+        self.codes = UnifiedTensor.empty(ctx, [copies, n, k], DType.I8)
+        self.scales = UnifiedTensor.empty(ctx, [copies, n], DType.FP32)
+        first = UnifiedTensor.new(ctx, q, dtype=DType.I8)
+        fs = UnifiedTensor.new(ctx, s)
+        for c in range(copies):
+            _lib.call("rq_memcpy_d2d", ctx.handle, self.codes.ptr + c * n * k, first.ptr, n * k, None)
+            _lib.call("rq_memcpy_d2d", ctx.handle, self.scales.ptr + c * n * 4, fs.ptr, n * 4, None)
+        ctx.sync()
+        self.x = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+        self.y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
+        self.desc = [_lib.rq_qweight(self.codes.ptr + c * n * k, self.scales.ptr + c * n * 4, None, n, k,
+                                     _lib.RQ_Q_ROWWISE_I8, 0) for c in range(copies)]
+        self._fn = _lib.lib().rq_qmatmul
+        self._h = ctx.handle
+        self.bytes = gemv_bytes(m, n, k)
+
+    def launch(self, i: int) -> None:
+        st = self._fn(self._h, ctypes.byref(self.desc[i % self.copies]), self.x.ptr, 1, self.y.ptr, 1, self.m, None)
+        if st != 0:
+            from rusty_amd import _lib
+            _lib.check(st, "rq_qmatmul")
+
+
+def time_steps(ctx, wl: GemvWorkload, steps: int, warmup: int, use_graph: bool = True):
+    """Times exactly `steps` launches; returns (wall ms, mean kernel ms)."""
+    from rusty_amd.hiprt import Event, Graph
+
+    stream = ctx.stream
+    graph = Graph(stream, lambda: [wl.launch(i) for i in range(wl.copies)]) if use_graph else None
+
+    def run(n: int) -> None:
+        i = 0
+        if graph is not None:
+            while n - i >= wl.copies:
+                graph.launch()
+                i += wl.copies
+        while i < n:
+            wl.launch(i)
+            i += 1
+
+    run(warmup)
+    ctx.sync()
+    t0, t1 = Event(), Event()
+    t0.record(stream)
+    run(steps)
+    t1.record(stream)
+    t1.synchronize()
+    wall_ms = t0.elapsed_ms(t1)
+    # mean kernel duration: one event pair around each of `probe` launches
+    probe = min(steps, 4 * wl.copies)
+    evs = [(Event(), Event()) for _ in range(probe)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        wl.launch(i)
+        b.record(stream)
+    evs[-1][1].synchronize()
+    kern_ms = float(np.mean([a.elapsed_ms(b) for a, b in evs]))
+    return wall_ms, kern_ms
+
+
+def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5):
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+    from rusty_amd.hiprt import Event
+
+    g = synth.rng(n + k)
+    q, s = synth.rowwise_weight(g, n, k)
+    w = QuantizedTensor.rowwise(ctx, q, s)
+    x = UnifiedTensor.new(ctx, synth.activations(g, m, k, sigma=0.5), dtype=DType.FP16)
+    y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
+    for _ in range(warmup):
+        engine.qmatmul(ctx, x, w, y)
+    ctx.sync()
+    a, b = Event(), Event()
+    a.record(ctx.stream)
+    for _ in range(steps):
+        engine.qmatmul(ctx, x, w, y)
+    b.record(ctx.stream)
+    b.synchronize()
+    ms = a.elapsed_ms(b) / steps
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"shape": f"{m}x{n}x{k}", "ms": round(ms, 5), "tflops": round(tflops, 2),
+            "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+
+
+def cpu_baseline(seconds: float):
+    """The reference's per-token Linear step on host cores (oracle port)."""
+    from oracle import oracle as orc
+    from rusty_amd import synth
+
+    g = synth.rng(0)
+    q, s = synth.rowwise_weight(g, 4096, 4096)
+    x = synth.activations(g, 1, 4096).astype(np.float32)
+    ref = orc.RefLinear(q, s, None, 0)  # load-time dequantization (untimed, as in the reference)
+    y = np.empty((1, 4096), np.float32)
+    _, threads = ref.forward(x, y)  # warm
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        ref.forward(x, y)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = gemv_bytes(1, 4096, 4096) * steps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": (f"{steps} per-token steps of the reference path (k-ascending f32 fma GEMV on the "
+                       f"load-time-dequantized f32 weight, configs[1] shape 4096x4096 M=1) in {el:.1f} s; "
+                       f"bytes counted as the int8 algorithmic bytes of the GPU step")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--prefill-steps", type=int, default=30)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch every step directly (no HIP graph)")
+    ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build's hot path runs on a single MI355X and has no "
+              "multi-GPU mode (see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from rusty_amd import ComputeEngine, WgpuContext
+
+    ctx = WgpuContext(0)
+    engine = ComputeEngine(ctx)
+    log(f"device 0: {ctx.num_cus} CUs")
+
+    wl = GemvWorkload(ctx, 1, 4096, 4096)
+    log("headline: GEMV 4096x4096 M=1, %d rotating copies" % wl.copies)
+    wall_ms, kern_ms = time_steps(ctx, wl, args.steps, args.warmup, use_graph=not args.no_graph)
+    ms_per_step = wall_ms / args.steps
+    value = wl.bytes * args.steps / (wall_ms * 1e-3) / 1e9
+    achieved = wl.bytes / (kern_ms * 1e-3) / 1e9
+    log(f"GEMV M=1: {value:.1f} GB/s whole-job, kernel {kern_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic (seeded numpy PCG64: int8 codes U[-127,127], scales U(0.001,0.02), X ~ N(0,1) fp16)",
+        "config": {"workload": "configs[1]: decode dequant-GEMV W int8 [4096,4096] per-row f32 scale, "
+                               "X fp16 [1,4096], Y fp16; 48 rotating weight copies (806 MB > 2x MALL)",
+                   "m": 1, "n": 4096, "k": 4096, "bytes_per_step": wl.bytes,
+                   "launch": "direct" if args.no_graph else "HIP graph of 48 launches"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv<M=1,CPT=1,TPR=256,rowwise,fp16>", "mean_kernel_us": round(kern_ms * 1e3, 3)},
+    }
+
+    if not args.quick:
+        extra = {}
+        for m, n, k in ((4, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 11008, 4096), (1, 4096, 11008),
+                        (8, 4096, 11008)):
+            copies = max(2, min(COPIES, (600 << 20) // (n * k)))
+            w2 = GemvWorkload(ctx, m, n, k, copies=copies)
+            wms, kms = time_steps(ctx, w2, 20 * copies, 2 * copies)
+            extra[f"m{m}_{n}x{k}"] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1),
+                                      "kernel_us": round(kms * 1e3, 2),
+                                      "wall_gbs": round(w2.bytes * 20 * copies / (wms * 1e-3) / 1e9, 1)}
+            log(f"GEMV m={m} {n}x{k}: {extra[f'm{m}_{n}x{k}']}")
+            del w2
+        result["decode_gemv"] = extra
+        pf = []
+        for n, k in ((4096, 4096), (11008, 4096), (4096, 11008)):
+            pf.append(prefill(ctx, engine, n, k, steps=args.prefill_steps))
+            log(f"prefill {pf[-1]}")
+        result["prefill"] = pf
+        result["decode_tok_s"] = None  # configs[4] (1.1B decode loop) not built yet
+
+    if not args.no_cpu_baseline:
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

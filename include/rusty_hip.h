@@ -1,0 +1,159 @@
+/*
+ * rusty_hip.h -- C ABI of the MI355X (gfx950) quantized-linear hot path.
+ *
+ * Drop-in for the op surface of Rusty's `ComputeEngine` on the int8
+ * quantized-linear path (rusty-backend/src/lib.rs).  Plain pointers and sizes,
+ * no C++ or torch types, bindgen-clean.  All tensor pointers are DEVICE
+ * pointers owned by the caller (the reference's caller-allocated `out`
+ * convention, rusty-autograd/src/lib.rs:468-477).  Every call returns an
+ * rq_status; nothing aborts.  Work is enqueued on a HIP stream (NULL = the
+ * context's own stream) and is asynchronous, like the reference's
+ * `queue.submit`; completion is observed with rq_sync (the reference's
+ * `device.poll(Wait)` inside `UnifiedTensor::to_vec`, lib.rs:215-240).
+ * A context is used from one host thread at a time (the reference's Tensor is
+ * RefCell-based and single-threaded, rusty-autograd/src/lib.rs:11-17).
+ */
+#ifndef RUSTY_HIP_H
+#define RUSTY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+typedef enum rq_status {
+    RQ_OK = 0,
+    RQ_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad enum, bad flag        */
+    RQ_ERR_SHAPE = -2,            /* sizes inconsistent or out of range      */
+    RQ_ERR_UNSUPPORTED = -3,      /* valid request this build does not serve */
+    RQ_ERR_HIP = -4,              /* a HIP runtime call failed               */
+    RQ_ERR_NO_DEVICE = -5,        /* no gfx950 device with that ordinal      */
+    RQ_ERR_ALLOC = -6             /* device or host allocation failed        */
+} rq_status;
+
+typedef enum rq_dtype { RQ_F32 = 0, RQ_F16 = 1 } rq_dtype;
+
+/* Quantized weight formats.
+ *  RQ_Q_ROWWISE_I8: signed int8 codes q[n,k], one f32 scale per output row:
+ *                   W[n,k] = f32(q[n,k]) * scales[n].
+ *  RQ_Q_AFFINE_U8 : the reference's MLX-style affine 8-bit format
+ *                   (rusty-backend/src/kernels.wgsl:379-400, loaded by
+ *                   rusty-loader/src/lib.rs:155-218): unsigned codes u,
+ *                   f32 scale and bias per `group` consecutive elements of the
+ *                   flattened row-major index i = n*k_in + k:
+ *                   W[i] = f32(u[i]) * scales[i/group] + biases[i/group]. */
+typedef enum rq_qformat { RQ_Q_ROWWISE_I8 = 0, RQ_Q_AFFINE_U8 = 1 } rq_qformat;
+
+/* A quantized Linear weight in [out, in] ("W[n_out, k_in]", K contiguous)
+ * orientation: Y = X . deq(W)^T, the semantics of the reference's `matmul_bt`
+ * (kernels.wgsl:234-242).  The reference has no int8 tensor type (its DType
+ * is {FP32, FP16}, lib.rs:57-76); quantized weights travel as raw buffer
+ * triplets (lib.rs:4939-4946).  This struct is that triplet plus its shape. */
+typedef struct rq_qweight {
+    const void *codes;    /* device, n_out*k_in bytes, row-major           */
+    const float *scales;  /* device, ROWWISE: [n_out]; AFFINE: [n_groups]  */
+    const float *biases;  /* device, AFFINE: [n_groups] or NULL (= 0)      */
+    int64_t n_out;
+    int64_t k_in;
+    int32_t format;       /* rq_qformat                                    */
+    int32_t group;        /* AFFINE: elements per group (64 in reference)  */
+} rq_qweight;
+
+typedef struct rq_ctx rq_ctx;
+typedef void *rq_stream; /* a hipStream_t; NULL selects the context stream */
+
+/* ---- context ------------------------------------------------------------
+ * Replaces WgpuContext::new (rusty-backend/src/lib.rs:20-47) +
+ * ComputeEngine::new (lib.rs:343-4017): selects the device, creates the
+ * context's stream (default priority).  Fails with RQ_ERR_NO_DEVICE unless
+ * the device is a gfx950. */
+int rq_ctx_create(int device, rq_ctx **out);
+int rq_ctx_destroy(rq_ctx *ctx);
+int rq_ctx_stream(rq_ctx *ctx, rq_stream *out);
+/* Number of compute units of the context's device. */
+int rq_ctx_num_cus(rq_ctx *ctx, int *out);
+/* Blocks until all work on `stream` is done (device.poll(Wait), lib.rs:232). */
+int rq_sync(rq_ctx *ctx, rq_stream stream);
+/* Human-readable name of a status code, and the calling thread's last error
+ * message (empty string if none). */
+const char *rq_status_string(int status);
+const char *rq_last_error(void);
+
+/* ---- memory --------------------------------------------------------------
+ * Replaces UnifiedTensor::{new, empty, to_vec} (lib.rs:115-240): device
+ * allocation, host->device upload, device->host readback.  Unlike the
+ * reference's pooled `empty()` (pool.rs:30-56, stale contents), rq_alloc
+ * memory is uninitialised and rq_memset clears it explicitly. */
+int rq_alloc(rq_ctx *ctx, size_t bytes, void **dptr);
+int rq_free(rq_ctx *ctx, void *dptr);
+int rq_memcpy_h2d(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream);
+int rq_memcpy_d2h(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream);
+int rq_memcpy_d2d(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream);
+int rq_memset(rq_ctx *ctx, void *dst, int value, size_t bytes, rq_stream stream);
+
+/* ---- dequantization --------------------------------------------------- */
+
+/* ComputeEngine::dequantize (lib.rs:4872-4899), kernel kernels.wgsl:153-166:
+ * out[4i+j] = f32((input[i] >> 8j) & 0xFF) for i < n_words, 4i+j < n_out
+ * (little-endian bytes, unsigned, no scale). */
+int rq_dequantize(rq_ctx *ctx, const uint32_t *input, size_t n_words, float *out, size_t n_out,
+                  rq_stream stream);
+
+/* ComputeEngine::affine_dequantize (lib.rs:4939-4990), kernel
+ * kernels.wgsl:379-400:
+ * out[i] = f32(byte_i) * scales[i/group] + biases[i/group], i < n_out.
+ * `group` is 64 in the reference (hard-coded at kernels.wgsl:395).
+ * Requires n_weight_words >= ceil(n_out/4), n_groups >= ceil(n_out/group).
+ * flags: 0 = multiply then add, each rounded to f32 (as the WGSL is written);
+ * RQ_AFFINE_FMA = one fused multiply-add (a shader compiler that contracts).
+ * Every element of out is written: the reference's 2-D dispatch fallback
+ * (lib.rs:4976-4987) leaves elements >= 4,194,240 unwritten; this does not. */
+#define RQ_AFFINE_FMA 1u
+int rq_affine_dequantize(rq_ctx *ctx, const uint32_t *weight, size_t n_weight_words,
+                         const float *scales, const float *biases, size_t n_groups, float *out,
+                         size_t n_out, uint32_t group, uint32_t flags, rq_stream stream);
+
+/* Dequantizes any rq_qweight to f32 [n_out, k_in] (ROWWISE: f32(q)*s, one
+ * rounding; AFFINE: as rq_affine_dequantize with flags 0).  The load-time
+ * step of WeightsContext::upload_quantized (rusty-loader/src/lib.rs:155-218)
+ * with the logical [out, in] shape (the reference allocates the packed
+ * shape, lib.rs:172-174,206). */
+int rq_qweight_dequantize(rq_ctx *ctx, const rq_qweight *w, float *out, rq_stream stream);
+
+/* ---- f32 matmul family (the reference's per-token GEMMs) ---------------
+ * All row-major f32, one f32 sum per output in ascending k, each step a fused
+ * multiply-add.  m, k, n as the host derives them from tensor shapes. */
+
+/* ComputeEngine::matmul (lib.rs:4403-4453), kernel `matmul_tiled`
+ * kernels.wgsl:7-54: out[m,n] = a[m,k] . b[k,n]. */
+int rq_matmul(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k,
+              int64_t n, rq_stream stream);
+/* ComputeEngine::matmul_bt (lib.rs:4299-4349), kernels.wgsl:234-242:
+ * out[m,n] = a[m,k] . b[n,k]^T. */
+int rq_matmul_bt(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k,
+                 int64_t n, rq_stream stream);
+/* ComputeEngine::matmul_at (lib.rs:4351-4401), kernels.wgsl:244-252:
+ * out[m,n] = a[k,m]^T . b[k,n]. */
+int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k,
+                 int64_t n, rq_stream stream);
+
+/* ---- fused quantized linear -------------------------------------------
+ * Y[m, n_out] = X[m, k_in] . deq(W)^T, dequantization fused into the
+ * product (int8 read straight from HBM, scale applied in registers).  This
+ * replaces the reference's two-step path -- load-time affine_dequantize to an
+ * f32 weight (rusty-loader/src/lib.rs:209) followed by `matmul` on every
+ * forward (Linear::forward, rusty-graph/src/lib.rs:69-70 ->
+ * Tensor::matmul, rusty-autograd/src/lib.rs:468-477).
+ * x_dtype/y_dtype: RQ_F16 or RQ_F32; accumulation is f32.
+ * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM. */
+int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y,
+               rq_dtype y_dtype, int64_t m, rq_stream stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* RUSTY_HIP_H */

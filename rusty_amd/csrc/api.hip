@@ -1,0 +1,290 @@
+// C-ABI layer: argument validation, context/stream/memory plumbing and
+// dispatch to the gfx950 kernels.  Declarations and the reference interface
+// each entry point replaces are in include/rusty_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "common.hpp"
+
+struct rq_ctx {
+    int device;
+    hipStream_t stream;
+    int num_cus;
+};
+
+namespace rq {
+
+static thread_local char g_err[512];
+
+int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+static int enter(rq_ctx *ctx) {
+    g_err[0] = '\0';
+    if (!ctx) return fail(RQ_ERR_INVALID_ARGUMENT, "null context");
+    int cur = -1;
+    RQ_HIP_TRY(hipGetDevice(&cur));
+    if (cur != ctx->device) RQ_HIP_TRY(hipSetDevice(ctx->device));
+    return RQ_OK;
+}
+
+static hipStream_t pick(rq_ctx *ctx, rq_stream s) { return s ? static_cast<hipStream_t>(s) : ctx->stream; }
+
+// a*b without overflow; false if it does not fit in int64.
+static bool mul_ok(int64_t a, int64_t b, int64_t *out) {
+    if (a < 0 || b < 0) return false;
+    if (a != 0 && b > INT64_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+}  // namespace rq
+
+using namespace rq;
+
+#define RQ_ENTER(ctx)                      \
+    do {                                   \
+        int rq_st_ = ::rq::enter(ctx);     \
+        if (rq_st_ != RQ_OK) return rq_st_; \
+    } while (0)
+
+extern "C" {
+
+const char *rq_status_string(int status) {
+    switch (status) {
+    case RQ_OK: return "RQ_OK";
+    case RQ_ERR_INVALID_ARGUMENT: return "RQ_ERR_INVALID_ARGUMENT";
+    case RQ_ERR_SHAPE: return "RQ_ERR_SHAPE";
+    case RQ_ERR_UNSUPPORTED: return "RQ_ERR_UNSUPPORTED";
+    case RQ_ERR_HIP: return "RQ_ERR_HIP";
+    case RQ_ERR_NO_DEVICE: return "RQ_ERR_NO_DEVICE";
+    case RQ_ERR_ALLOC: return "RQ_ERR_ALLOC";
+    default: return "RQ_ERR_UNKNOWN";
+    }
+}
+
+const char *rq_last_error(void) { return g_err; }
+
+int rq_ctx_create(int device, rq_ctx **out) {
+    g_err[0] = '\0';
+    if (!out) return fail(RQ_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(RQ_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(RQ_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, count);
+    hipDeviceProp_t prop;
+    RQ_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(RQ_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", device,
+                    prop.gcnArchName);
+    RQ_HIP_TRY(hipSetDevice(device));
+    rq_ctx *ctx = new (std::nothrow) rq_ctx;
+    if (!ctx) return fail(RQ_ERR_ALLOC, "context allocation failed");
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    // Default priority on purpose: streams of mixed priorities are not used.
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(RQ_ERR_HIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
+    }
+    *out = ctx;
+    return RQ_OK;
+}
+
+int rq_ctx_destroy(rq_ctx *ctx) {
+    if (!ctx) return RQ_OK;
+    RQ_ENTER(ctx);
+    hipError_t e1 = hipStreamSynchronize(ctx->stream);
+    hipError_t e2 = hipStreamDestroy(ctx->stream);
+    delete ctx;
+    if (e1 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e1));
+    if (e2 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamDestroy: %s", hipGetErrorString(e2));
+    return RQ_OK;
+}
+
+int rq_ctx_stream(rq_ctx *ctx, rq_stream *out) {
+    RQ_ENTER(ctx);
+    if (!out) return fail(RQ_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = ctx->stream;
+    return RQ_OK;
+}
+
+int rq_ctx_num_cus(rq_ctx *ctx, int *out) {
+    RQ_ENTER(ctx);
+    if (!out) return fail(RQ_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = ctx->num_cus;
+    return RQ_OK;
+}
+
+int rq_sync(rq_ctx *ctx, rq_stream stream) {
+    RQ_ENTER(ctx);
+    RQ_HIP_TRY(hipStreamSynchronize(pick(ctx, stream)));
+    return RQ_OK;
+}
+
+int rq_alloc(rq_ctx *ctx, size_t bytes, void **dptr) {
+    RQ_ENTER(ctx);
+    if (!dptr) return fail(RQ_ERR_INVALID_ARGUMENT, "null output pointer");
+    *dptr = nullptr;
+    if (bytes == 0) return RQ_OK;
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        return fail(RQ_ERR_ALLOC, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    return RQ_OK;
+}
+
+int rq_free(rq_ctx *ctx, void *dptr) {
+    RQ_ENTER(ctx);
+    if (!dptr) return RQ_OK;
+    RQ_HIP_TRY(hipFree(dptr));
+    return RQ_OK;
+}
+
+static int copy(rq_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (bytes == 0) return RQ_OK;
+    if (!dst || !src) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer in copy");
+    hipStream_t s = pick(ctx, stream);
+    RQ_HIP_TRY(hipMemcpyAsync(dst, src, bytes, kind, s));
+    // Host buffers are pageable and owned by the caller: complete the copy
+    // before returning, as UnifiedTensor::new / to_vec do.
+    if (kind != hipMemcpyDeviceToDevice) RQ_HIP_TRY(hipStreamSynchronize(s));
+    return RQ_OK;
+}
+
+int rq_memcpy_h2d(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream) {
+    return copy(ctx, dst, src, bytes, hipMemcpyHostToDevice, stream);
+}
+int rq_memcpy_d2h(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost, stream);
+}
+int rq_memcpy_d2d(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, stream);
+}
+
+int rq_memset(rq_ctx *ctx, void *dst, int value, size_t bytes, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (bytes == 0) return RQ_OK;
+    if (!dst) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer in memset");
+    RQ_HIP_TRY(hipMemsetAsync(dst, value, bytes, pick(ctx, stream)));
+    return RQ_OK;
+}
+
+int rq_dequantize(rq_ctx *ctx, const uint32_t *input, size_t n_words, float *out, size_t n_out,
+                  rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (n_words == 0 || n_out == 0) return RQ_OK;
+    if (!input || !out) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (n_words > SIZE_MAX / 4) return fail(RQ_ERR_SHAPE, "n_words too large");
+    return launch_dequantize(input, n_words, out, n_out, pick(ctx, stream));
+}
+
+int rq_affine_dequantize(rq_ctx *ctx, const uint32_t *weight, size_t n_weight_words, const float *scales,
+                         const float *biases, size_t n_groups, float *out, size_t n_out, uint32_t group,
+                         uint32_t flags, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (flags & ~RQ_AFFINE_FMA) return fail(RQ_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (group == 0) return fail(RQ_ERR_INVALID_ARGUMENT, "group must be > 0");
+    if (n_out == 0) return RQ_OK;
+    if (!weight || !scales || !out) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (n_weight_words < (n_out + 3) / 4)
+        return fail(RQ_ERR_SHAPE, "weight has %zu words, %zu elements need %zu", n_weight_words, n_out,
+                    (n_out + 3) / 4);
+    if (n_groups < (n_out + group - 1) / group)
+        return fail(RQ_ERR_SHAPE, "%zu scale groups, %zu elements need %zu", n_groups, n_out,
+                    (n_out + group - 1) / group);
+    return launch_affine_dequantize(weight, scales, biases, out, n_out, group, (flags & RQ_AFFINE_FMA) != 0,
+                                    pick(ctx, stream));
+}
+
+static int check_qweight(const rq_qweight *w) {
+    if (!w) return fail(RQ_ERR_INVALID_ARGUMENT, "null weight");
+    if (w->format != RQ_Q_ROWWISE_I8 && w->format != RQ_Q_AFFINE_U8)
+        return fail(RQ_ERR_INVALID_ARGUMENT, "unknown weight format %d", w->format);
+    if (w->n_out < 0 || w->k_in < 0) return fail(RQ_ERR_SHAPE, "negative weight shape");
+    int64_t n;
+    if (!mul_ok(w->n_out, w->k_in, &n)) return fail(RQ_ERR_SHAPE, "weight shape overflows");
+    if (w->format == RQ_Q_AFFINE_U8 && w->group <= 0)
+        return fail(RQ_ERR_INVALID_ARGUMENT, "affine weight needs group > 0");
+    if (n > 0 && !w->codes) return fail(RQ_ERR_INVALID_ARGUMENT, "null codes");
+    if (w->n_out > 0 && !w->scales) return fail(RQ_ERR_INVALID_ARGUMENT, "null scales");
+    return RQ_OK;
+}
+
+int rq_qweight_dequantize(rq_ctx *ctx, const rq_qweight *w, float *out, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    const size_t n = (size_t)w->n_out * (size_t)w->k_in;
+    if (n == 0) return RQ_OK;
+    if (!out) return fail(RQ_ERR_INVALID_ARGUMENT, "null output");
+    if (w->format == RQ_Q_ROWWISE_I8)
+        return launch_rowwise_dequantize((const int8_t *)w->codes, w->scales, out, w->n_out, w->k_in,
+                                         pick(ctx, stream));
+    // The affine kernel reads the codes as u32 words; a byte count that is
+    // not a multiple of 4 would make its last word read past the buffer, so
+    // such tails take the byte path inside the kernel (n bounds every read).
+    return launch_affine_dequantize((const uint32_t *)w->codes, w->scales, w->biases, out, n, (uint32_t)w->group,
+                                    false, pick(ctx, stream));
+}
+
+static int matmul_common(rq_ctx *ctx, int variant, const float *a, const float *b, float *out, int64_t m,
+                         int64_t k, int64_t n, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (m < 0 || k < 0 || n < 0) return fail(RQ_ERR_SHAPE, "negative matmul shape");
+    int64_t t;
+    if (!mul_ok(m, k, &t) || !mul_ok(k, n, &t) || !mul_ok(m, n, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0 || n == 0) return RQ_OK;
+    if (!out || (k > 0 && (!a || !b))) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer");
+    return launch_matmul_f32(variant, a, b, out, m, k, n, pick(ctx, stream));
+}
+
+int rq_matmul(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
+              rq_stream stream) {
+    return matmul_common(ctx, MM_AB, a, b, out, m, k, n, stream);
+}
+int rq_matmul_bt(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
+                 rq_stream stream) {
+    return matmul_common(ctx, MM_ABT, a, b, out, m, k, n, stream);
+}
+int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
+                 rq_stream stream) {
+    return matmul_common(ctx, MM_ATB, a, b, out, m, k, n, stream);
+}
+
+int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y, rq_dtype y_dtype,
+               int64_t m, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    if ((x_dtype != RQ_F16 && x_dtype != RQ_F32) || (y_dtype != RQ_F16 && y_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
+    int64_t t;
+    if (!mul_ok(m, w->k_in, &t) || !mul_ok(m, w->n_out, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0 || w->n_out == 0) return RQ_OK;
+    if (!y || (w->k_in > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
+    hipStream_t s = pick(ctx, stream);
+    if (w->k_in > 0) {
+        st = RQ_ERR_UNSUPPORTED;
+        if (m <= 8) st = launch_gemv(*w, x, x_dtype, y, y_dtype, (int)m, ctx->num_cus, s);
+        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(*w, x, x_dtype, y, y_dtype, m, ctx->num_cus, s);
+        if (st != RQ_ERR_UNSUPPORTED) return st;
+    }
+    return launch_qlinear_generic(*w, x, x_dtype, y, y_dtype, m, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,216 @@
+"""GPU parity of the fused quantized linear (rq_qmatmul) against the oracle's
+f64 truth of Y = X . deq(W)^T.
+
+Tolerances (stated here, reported by every test):
+  * f32 output: max|dy| / max|y| <= 1e-5
+  * fp16 output: |dy| <= 2e-3*|y| + 2e-3*max|y| elementwise
+The truth is computed from the same fp16-rounded X and the exactly dequantized
+weight.  Full prefill sizes are checked on sampled rows that cover every
+128-row tile and every row position inside a tile, plus a column-checksum
+(sum over all tokens, a linear invariant) that covers every output row.
+"""
+import numpy as np
+import pytest
+
+from conftest import f16_tol_check, f32_norm_check
+from oracle import oracle as orc
+from rusty_amd import DType, QuantizedTensor, RqError, UnifiedTensor, synth
+
+pytestmark = pytest.mark.gpu
+
+F = {np.float16: DType.FP16, np.float32: DType.FP32}
+
+
+def qmm(ctx, engine, w, x, ydt):
+    X = UnifiedTensor.new(ctx, x, dtype=F[x.dtype.type])
+    Y = UnifiedTensor.new(ctx, np.full((x.shape[0], w.n_out), np.nan, ydt), dtype=F[ydt])
+    engine.qmatmul(ctx, X, w, Y)
+    return Y.to_vec()
+
+
+def report(name, max_abs, rel):
+    print(f"[{name}] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+
+
+# ---- config 1: C1 int8 [1024,1024] x f32 [8,1024] -> f32 ----------------------
+
+def test_config1_rowwise_f32(ctx, engine):
+    g = synth.rng(0)
+    q, s = synth.rowwise_weight(g, 1024, 1024)
+    x = synth.activations(g, 8, 1024, dtype=np.float32)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float32)
+    truth = orc.qlinear_truth(q, s, None, x, 0)
+    max_abs, rel, ok = f32_norm_check(y, truth)
+    ref_y, _ = orc.ref_linear(q, s, None, x, 0)  # the reference's own f32 rounding order
+    report("C1 rowwise f32", max_abs, rel)
+    print(f"   vs reference-order f32: max_abs={np.abs(y - ref_y).max():.3e}", flush=True)
+    assert ok
+
+
+def test_config1_affine_reference_format_f32(ctx, engine):
+    g = synth.rng(0)
+    u, s, b = synth.affine_weight(g, 1024, 1024)
+    x = synth.activations(g, 8, 1024, dtype=np.float32)
+    y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float32)
+    truth = orc.qlinear_truth(u, s, b, x, 1)
+    max_abs, rel, ok = f32_norm_check(y, truth)
+    report("C1 affine f32", max_abs, rel)
+    assert ok
+
+
+# ---- decode GEMV (m <= 16) ---------------------------------------------------
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_config2_decode_4096(ctx, engine, m):
+    g = synth.rng(100 + m)
+    q, s = synth.rowwise_weight(g, 4096, 4096)
+    x = synth.activations(g, m, 4096)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    truth = orc.qlinear_truth(q, s, None, x.astype(np.float32), 0)
+    max_abs, rel, ok = f16_tol_check(y, truth)
+    report(f"C2 m={m}", max_abs, rel)
+    assert ok
+
+
+@pytest.mark.parametrize("k", [1024, 2048, 4096, 5632, 11008])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 12])
+def test_gemv_shapes(ctx, engine, m, k):
+    g = synth.rng(m * 100000 + k)
+    n = 200  # not a multiple of the row batch
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok, (max_abs, rel)
+
+
+@pytest.mark.parametrize("k", [1024, 4096, 11008])
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_gemv_affine_reference_format(ctx, engine, m, k):
+    g = synth.rng(m + k)
+    u, s, b = synth.affine_weight(g, 136, k)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(u, s, b, x.astype(np.float32), 1))
+    assert ok, (max_abs, rel)
+
+
+@pytest.mark.parametrize("ydt", [np.float16, np.float32])
+def test_gemv_f32_output_and_activations(ctx, engine, ydt):
+    g = synth.rng(42)
+    q, s = synth.rowwise_weight(g, 333, 2048)
+    x = synth.activations(g, 2, 2048, dtype=np.float32)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, ydt)
+    truth = orc.qlinear_truth(q, s, None, x, 0)
+    _, _, ok = f32_norm_check(y, truth) if ydt is np.float32 else f16_tol_check(y, truth)
+    assert ok
+
+
+def test_swiglu_shapes_m8(ctx, engine):
+    g = synth.rng(3)
+    for n, k in ((11008, 4096), (4096, 11008)):
+        q, s = synth.rowwise_weight(g, n, k)
+        x = synth.activations(g, 8, k)
+        y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+        max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+        report(f"swiglu-shape {n}x{k} m=8", max_abs, rel)
+        assert ok
+
+
+# ---- prefill GEMM (MFMA) -------------------------------------------------------
+
+def _sample_rows(m, tile=128, per_tile=8):
+    rows = set()
+    for b in range(-(-m // tile)):
+        for j in range(per_tile):
+            r = b * tile + (b * per_tile + j) % tile
+            if r < m:
+                rows.add(r)
+    rows.update({0, m - 1})
+    return np.array(sorted(rows))
+
+
+def _check_prefill(y, x, q, s, name):
+    rows = _sample_rows(x.shape[0])
+    truth = orc.qlinear_truth(q, s, None, x[rows].astype(np.float32), 0)
+    max_abs, rel, ok = f16_tol_check(y[rows], truth)
+    report(f"{name} sampled {len(rows)} rows", max_abs, rel)
+    assert ok
+    # column checksum over all tokens: sum_m Y[m, n] = (sum_m X[m, :]) . w[n, :]
+    xsum = x.astype(np.float64).sum(axis=0, keepdims=True)
+    col_truth = orc.qlinear_truth(q, s, None, xsum.astype(np.float32), 0)[0]
+    xsum_err = np.abs(xsum - xsum.astype(np.float32).astype(np.float64))  # f32 rounding of the summed X
+    w_abs = np.abs(q.astype(np.float64)) * s[:, None].astype(np.float64)
+    col_dev = y.astype(np.float64).sum(axis=0)
+    # fp16 output rounding of each element is <= 2^-11 |y|, independent across tokens
+    sigma = np.sqrt(((2.0 ** -11 * y.astype(np.float64)) ** 2).sum(axis=0) / 3)
+    bound = 8 * sigma + w_abs @ xsum_err[0] + 1e-5 * np.abs(y.astype(np.float64)).sum(axis=0)
+    assert np.all(np.abs(col_dev - col_truth) <= bound), float((np.abs(col_dev - col_truth) / bound).max())
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (11008, 4096), (4096, 11008)])
+def test_config4_prefill(ctx, engine, n, k):
+    g = synth.rng(n + k)
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, 2048, k, sigma=0.5)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    assert np.isfinite(y).all()
+    _check_prefill(y, x, q, s, f"C4 2048x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 136, 2048), (300, 4096, 64), (129, 129, 128)])
+def test_gemm_ragged(ctx, engine, m, n, k):
+    g = synth.rng(m + n + k)
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok, (max_abs, rel)
+
+
+# ---- generic path, edge cases, errors -------------------------------------------
+
+@pytest.mark.parametrize("m,n,k,fmt", [(1, 50, 1000, 0), (3, 7, 33, 0), (20, 31, 100, 0), (2, 40, 96, 1),
+                                       (64, 64, 4096, 1)])
+def test_generic_path(ctx, engine, m, n, k, fmt):
+    g = synth.rng(m * n + k)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n, k)
+        b = None
+        w = QuantizedTensor.rowwise(ctx, q, s)
+    else:
+        q, s, b = synth.affine_weight(g, n, k)
+        w = QuantizedTensor.affine(ctx, q, s, b)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, w, x, np.float32)
+    _, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, b, x.astype(np.float32), fmt))
+    assert ok, rel
+
+
+def test_unaligned_activation_pointer(ctx, engine):
+    g = synth.rng(9)
+    q, s = synth.rowwise_weight(g, 64, 1024)
+    x = synth.activations(g, 1, 1024)
+    X = UnifiedTensor.new(ctx, np.concatenate([np.zeros(1, np.float16), x.ravel()]), dtype=DType.FP16)
+    xv = UnifiedTensor(ctx, X.ptr + 2, [1, 1024], DType.FP16, owner=False)
+    Y = UnifiedTensor.empty(ctx, [1, 64], DType.FP16)
+    engine.qmatmul(ctx, xv, QuantizedTensor.rowwise(ctx, q, s), Y)
+    _, _, ok = f16_tol_check(Y.to_vec(), orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok
+
+
+def test_zero_k_gives_zero(ctx, engine):
+    w = QuantizedTensor.rowwise(ctx, np.zeros((5, 0), np.int8), np.ones(5, np.float32))
+    X = UnifiedTensor.empty(ctx, [2, 0], DType.FP16)
+    Y = UnifiedTensor.new(ctx, np.full((2, 5), 7.0, np.float16), dtype=DType.FP16)
+    engine.qmatmul(ctx, X, w, Y)
+    assert np.all(Y.to_vec() == 0)
+
+
+def test_invalid_weight_format_raises(ctx, engine):
+    w = QuantizedTensor.rowwise(ctx, np.zeros((4, 16), np.int8), np.ones(4, np.float32))
+    w.format = 7
+    X = UnifiedTensor.empty(ctx, [1, 16], DType.FP16)
+    Y = UnifiedTensor.empty(ctx, [1, 4], DType.FP16)
+    with pytest.raises(RqError, match="INVALID_ARGUMENT"):
+        engine.qmatmul(ctx, X, w, Y)
