@@ -1,0 +1,251 @@
+// Decode dequant-GEMV, fp16 activations, m <= 4:  Y[m, n] = sum_k X[m, k] * deq(W)[n, k].
+//
+// HBM-bound: every weight byte is read once, 16.8 MB for a 4096x4096 layer,
+// a few microseconds per call.  At that size the fixed costs of a launch (wave
+// dispatch, first-byte latency, the reduction tail) are a large part of the
+// time, so the kernel is shaped around them (measured on MI355X, one-shot
+// 16 MB reads: ~3.8-4.1 us floor):
+//  * One block of 256 threads owns R*RP rows.  Thread tt of a row group (TPR
+//    threads) owns the 16-byte chunks tt, tt+TPR, ... of each of its rows, so
+//    every wave-wide load is 1 KiB contiguous in one row -- the access
+//    pattern that streams best (row-interleaved patterns measured 1.3-3x
+//    slower).  Many small blocks spread the dispatch over all 256 CUs.
+//  * Loads are buffer loads: the X slice first (cached), then all R*CPT weight
+//    chunks with the non-temporal policy (the weights are read once).  Rows
+//    past N and chunks past K are offsets past the buffer resource, which the
+//    hardware returns as zeros: no branches around the loads.
+//  * int8 -> fp16 is exact and convert-free: XOR 0x80 gives q+128, v_perm_b32
+//    puts it under exponent 0x64 -> fp16 1152+q; v_dot2_f32_f16 multiplies
+//    with X in f32; the lane subtracts 1152 * (sum of its X slice) once.
+//    Affine (reference) codes skip the XOR: fp16 1024+u, and per chunk the
+//    lane applies its group's scale s and bias b:
+//    acc += s * sum (1024+u) x + (b - 1024 s) * sum x.
+//  * Reduction: every thread stores its R*M partials to LDS; after one
+//    barrier each wave owns whole (row, token) tasks: TPR partials are summed
+//    with LDS reads + four DPP row steps + four readlanes, with no LDS
+//    round trip per row and no cross-lane shuffles.
+#include "common.hpp"
+
+namespace rq {
+namespace {
+
+constexpr int DT = 256;
+constexpr uint32_t kOOB = 0x80000000u;  // any offset past a resource reads zero
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+// aux bit 1 = non-temporal (streamed once), 0 = default caching
+template <int AUX>
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+__device__ __forceinline__ uint32_t magic_lo(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u); }
+__device__ __forceinline__ uint32_t magic_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// Sum over the 64 lanes, result uniform (scalar) across the wave.
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror: each 16-lane row holds its sum
+    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+// M: activation rows (m_act <= M); CPT: chunks per thread; TPR: threads per
+// row group; R: rows per row group; FMT: 0 = ROWWISE_I8, 1 = AFFINE_U8.
+template <int M, int CPT, int TPR, int R, int FMT>
+__global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
+                                                    const float *__restrict__ biases,
+                                                    const _Float16 *__restrict__ X, void *__restrict__ Yv,
+                                                    int y_f16, int m_act, int N, int K, int group) {
+    constexpr int RP = DT / TPR;
+    constexpr int ROWS = R * RP;
+    constexpr int TASKS = ROWS * M;
+    __shared__ float part[TASKS][TPR];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int rp = t / TPR, tt = t % TPR;
+    const int C = K >> 4;
+    const int row0 = blockIdx.x * ROWS;
+
+    // X slice (issued first so its wait does not cover the weight stream).
+    const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
+    uint32_t xh[CPT][M][8];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tt + TPR * j;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const uint32_t off = c < C ? ((uint32_t)m * K + (uint32_t)c * 16) * 2u : kOOB;
+            const uint4 a = bload<0>(rx, off), b = bload<0>(rx, off + 16);
+            xh[j][m][0] = a.x; xh[j][m][1] = a.y; xh[j][m][2] = a.z; xh[j][m][3] = a.w;
+            xh[j][m][4] = b.x; xh[j][m][5] = b.y; xh[j][m][6] = b.z; xh[j][m][7] = b.w;
+        }
+    }
+    // Weight chunks: R rows x CPT chunks per thread, all in flight.
+    const int rows_here = min(ROWS, N - row0);
+    const auto rw = make_rsrc(W + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
+    uint4 w[R][CPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+            const uint32_t off = c < C ? (uint32_t)(r * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
+            w[r][j] = bload<2>(rw, off);
+        }
+    float sg[R][CPT], bg[R][CPT];
+    if constexpr (FMT == 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int c = tt + TPR * j, rin = r * RP + rp;
+                sg[r][j] = 0.0f;
+                bg[r][j] = 0.0f;
+                if (c < C && rin < rows_here) {
+                    const size_t g = ((size_t)(row0 + rin) * K + (size_t)c * 16) / (size_t)group;
+                    sg[r][j] = scales[g];
+                    bg[r][j] = biases ? biases[g] : 0.0f;
+                }
+            }
+    }
+
+    // Per-chunk sums of X (fp16 dot with (1,1)); zero for chunks past K.
+    float xs[CPT][M], xs_tot[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) xs_tot[m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = dot2(xh[j][m][i], 0x3C003C00u, s);
+            xs[j][m] = s;
+            xs_tot[m] += s;
+        }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float p[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) p[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const uint32_t wd[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
+            float d[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) d[m] = FMT == 0 ? p[m] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t u = FMT == 0 ? (wd[q] ^ 0x80808080u) : wd[q];
+                const uint32_t lo = magic_lo(u), hi = magic_hi(u);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    d[m] = dot2(lo, xh[j][m][2 * q], d[m]);
+                    d[m] = dot2(hi, xh[j][m][2 * q + 1], d[m]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if constexpr (FMT == 0) {
+                    p[m] = d[m];
+                } else {
+                    const float s = sg[r][j];
+                    p[m] = __builtin_fmaf(s, d[m], p[m]);
+                    p[m] = __builtin_fmaf(__builtin_fmaf(-1024.0f, s, bg[r][j]), xs[j][m], p[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float v = FMT == 0 ? __builtin_fmaf(-1152.0f, xs_tot[m], p[m]) : p[m];
+            part[(r * RP + rp) * M + m][tt] = v;
+        }
+    }
+    __syncthreads();
+
+    // Each wave finishes whole (row, token) tasks.
+    for (int task = wave; task < TASKS; task += DT / 64) {
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TPR / 64; ++i) v += part[task][lane + 64 * i];
+        const float tot = wave_total(v);
+        const int rin = task / M, m = task % M;
+        const int row = row0 + rin;
+        if (lane == 0 && rin < rows_here && m < m_act) {
+            const float y = FMT == 0 ? tot * scales[row] : tot;
+            const size_t o = (size_t)m * N + row;
+            if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
+            else reinterpret_cast<float *>(Yv)[o] = y;
+        }
+    }
+}
+
+using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const _Float16 *, void *, int, int, int, int,
+                          int);
+
+template <int M, int CPT, int TPR>
+DecodeFn pick_fmt(int fmt) {
+    constexpr int R = M == 1 ? 2 : 4;
+    return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, R, 0> : &k_gemv_decode<M, CPT, TPR, R, 1>;
+}
+
+template <int M, int CPT>
+DecodeFn pick_tpr(int tpr, int fmt) {
+    switch (tpr) {
+    case 64: return pick_fmt<M, CPT, 64>(fmt);
+    case 128: return pick_fmt<M, CPT, 128>(fmt);
+    default: return pick_fmt<M, CPT, 256>(fmt);
+    }
+}
+
+template <int M>
+DecodeFn pick_cpt(int cpt, int tpr, int fmt) {
+    switch (cpt) {
+    case 1: return pick_tpr<M, 1>(tpr, fmt);
+    case 2: return pick_tpr<M, 2>(tpr, fmt);
+    case 3: return pick_tpr<M, 3>(tpr, fmt);
+    default: return pick_tpr<M, 4>(tpr, fmt);
+    }
+}
+
+}  // namespace
+
+int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
+    const int64_t N = w.n_out, K = w.k_in;
+    if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
+        !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && w.group % 16 != 0))
+        return RQ_ERR_UNSUPPORTED;
+    const int C = (int)(K / 16);
+    const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
+    const int cpt = (int)cdiv(C, tpr);
+    const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
+    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, w.format) : mt == 2 ? pick_cpt<2>(cpt, tpr, w.format)
+                                                                       : pick_cpt<4>(cpt, tpr, w.format);
+    const int rows = (mt == 1 ? 2 : 4) * (DT / tpr);
+    const int64_t blocks = cdiv(N, rows);
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
+                       (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.group);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+}  // namespace rq
