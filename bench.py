@@ -133,6 +133,21 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
             "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
 
 
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE passes, each calibrated against a
+    plain 16 MiB copy); None if the summary is absent or names another kernel."""
+    import pathlib
+    import re
+
+    p = pathlib.Path(__file__).resolve().parent / "profiles" / "gemv_decode_m1_4096x4096_pmc.md"
+    if not p.exists():
+        return None
+    text = p.read_text()
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    return int(m.group(1)) if m and kernel in text else None
+
+
 def cpu_baseline(seconds: float):
     """The reference's per-token Linear step on host cores (oracle port)."""
     from oracle import oracle as orc
@@ -208,8 +223,9 @@ def main() -> int:
                    "m": 1, "n": 4096, "k": 4096, "bytes_per_step": wl.bytes,
                    "launch": "direct" if args.no_graph else "HIP graph of 48 launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_decode<M=1,CPT=1,TPR=256,R=2,rowwise>",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile("k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>"),
+                     "kernel": "k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>",
                      "mean_launch_us": round(kern_ms * 1e3, 3),
                      "timing": "HIP events around the timed region on the launch stream / steps"},
     }
