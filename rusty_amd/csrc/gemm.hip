@@ -4,34 +4,68 @@
 // (rusty-backend/src/kernels.wgsl:7-54) on a load-time-dequantized weight
 // (kernels.wgsl:379-400).  MFMA-bound: 2*M*N*K flops over 1 B/weight + 2 B/act.
 //
-//  * Block tile 128 (X rows) x 128 (W rows) x 64 (k), 256 threads = 4 waves
-//    in a 2x2 grid, each wave 64x64 = 4x4 tiles of v_mfma_f32_16x16x32_f16
-//    with f32 accumulators.
-//  * Operands: MFMA A = W (16 output features x 32 k), B = X^T (32 k x 16
-//    tokens).  The f32 result of a tile then sits as 4 consecutive features of
-//    one token per lane, so the epilogue stores 8 B (fp16) per lane.
-//  * Staging: global -> registers -> LDS, double-buffered, one barrier per
-//    k-tile; the next tile's global loads are in flight while the current
-//    tile is multiplied.  LDS rows are padded (X: 144 B, W: 72 B) so the
-//    16 rows read by one MFMA operand fall in distinct banks.
-//  * int8 stays int8 in LDS (half the bytes of fp16) and is expanded right
-//    before the MFMA: XOR 0x80 turns q into q+128, v_perm_b32 builds fp16
-//    1024 + (q+128) = 1152 + q, v_pk_add_f16 subtracts 1152.  Exact.
-//  * Epilogue: per-feature scale (f32), convert, store.
+// Design (each choice measured on MI355X):
+//  * Block tile BM tokens x BN features, 64 k per step, 4 waves in 2x2, each
+//    wave (BM/2) x (BN/2) outputs as 32x32 tiles of v_mfma_f32_32x32x16_f16
+//    (the 32x32x16 form keeps the MFMA pipe ~82% busy from one wave per SIMD;
+//    16x16x32 only ~50%).  MFMA A = W (32 features x 16 k), B = X^T (16 k x
+//    32 tokens): a lane's accumulator holds runs of 4 consecutive features of
+//    one token (8-byte fp16 stores).
+//  * Staging is direct-to-LDS DMA (buffer_load_dwordx4 ... lds): each wave
+//    moves 1 KiB units from global memory straight into LDS, so tiles never
+//    pass through VGPRs or ds_write (register staging measured ~10% slower,
+//    limited by LDS write issue).  The weight stays int8 in LDS (half the
+//    bytes) and is expanded to fp16 when a wave reads its fragment:
+//    XOR 0x80 -> q+128, v_perm_b32 under exponent 0x64 -> fp16 1152+q,
+//    v_pk_add_f16 -1152 -> q (exact).
+//  * A 3-stage LDS ring, one barrier per k-step.  The loads of a stage are
+//    waited for with an explicit vmcnt (loads retire in order), so the DMA of
+//    the next steps stays in flight.  PINGPONG: the fragments of step k+1 are
+//    read into registers while the MFMAs of step k run.
+//  * LDS layouts are XOR-swizzled per 16-byte chunk (the DMA writes 1 KiB
+//    contiguous per wave, so padding is impossible): X rows (128 B) put chunk
+//    c at c ^ ((row >> 1) & 7), W rows (64 B) at c ^ ((row >> 2) & 3), which
+//    spreads the 32 rows an MFMA operand reads over the banks.
+//  * Rows past M/N and k past K are offsets past the buffer resource and read
+//    as zero: no branches around the loads; the k loop is padded to the ring
+//    period with zero steps.
+//  * XCD-aware tile order: the hardware deals consecutive blocks round-robin
+//    to the 8 XCDs, so block b takes tile (b % 8) * (tiles / 8) + b / 8; one
+//    XCD's tiles are then consecutive in token-major order and share their X
+//    panel in that XCD's L2.
 #include "common.hpp"
 
 namespace rq {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, TH = 256;
-constexpr int XS_STRIDE = BK * 2 + 16;  // bytes per X row in LDS
-constexpr int WS_STRIDE = BK + 8;       // bytes per W row in LDS
-constexpr int XS_BYTES = BM * XS_STRIDE;
-constexpr int WS_BYTES = BN * WS_STRIDE;
+constexpr int TH = 256;
+constexpr uint32_t kOOB = 0x80000000u;  // any offset past a buffer resource reads zero
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+
+// DMA of 16 bytes per lane: LDS[lds_base + 16 * lane] = buffer[voff].  Issued
+// as inline asm so the compiler does not turn its conservative LDS-DMA alias
+// tracking into a full vmcnt(0) wait before every LDS read; every reader of a
+// stage waits with an explicit s_waitcnt vmcnt instead.  M0 carries the LDS
+// base (one wait state before the load, as the ISA requires).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void *lds_base, uint32_t voff) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)lds_base);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
+// s_waitcnt immediate for "at most n vector-memory operations outstanding"
+// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14]).
+constexpr int vmcnt_le(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
 __device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t u, uint32_t sel) {
     const uint32_t m = __builtin_amdgcn_perm(0x64646464u, u, sel);
@@ -50,124 +84,191 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
     return __builtin_bit_cast(half8, r);
 }
 
+// One ring stage: X tile (BM rows x 64 fp16) and W tile (BN rows x 64 int8).
+// Three separate arrays, so each stage is a distinct LDS object.
+template <int BM, int BN>
+struct Stage {
+    uint8_t x[BM * 128];
+    uint8_t w[BN * 64];
+};
+
+template <int BM, int BN, bool PINGPONG>
 __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
-                                                     int y_f16, int M, int N, int K) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (XS_BYTES + WS_BYTES)];
+                                                     int y_f16, int M, int N, int K, int tiles_m, int tiles_n) {
+    constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
+    constexpr int XUW = BM * 128 / 1024 / 4, WUW = BN * 64 / 1024 / 4;  // 1 KiB DMA units per wave
+    static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
+    constexpr int NOUT = XUW + WUW;  // DMA ops per wave per k-step
 
-    const int t = threadIdx.x;
-    const int wave = t / 64, lane = t % 64;
-    const int wm = wave / 2, wn = wave % 2;  // wave tile: rows wm*64 of X, wn*64 of W
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    __shared__ __attribute__((aligned(1024))) Stage<BM, BN> s0;
+    __shared__ __attribute__((aligned(1024))) Stage<BM, BN> s1;
+    __shared__ __attribute__((aligned(1024))) Stage<BM, BN> s2;
 
-    // global -> register mapping
-    // X tile 128 x 64 fp16: thread covers rows t/8 + 32p (p<4), 16 B at col (t%8)*8
-    // W tile 128 x 64 i8  : thread covers rows t/4 + 64p (p<2), 16 B at col (t%4)*16
-    const int xr = t / 8, xc = (t % 8) * 8;
-    const int wr = t / 4, wc = (t % 4) * 16;
+    const int tiles = tiles_m * tiles_n, b = blockIdx.x;
+    const int tile = (tiles % 8 == 0) ? (b % 8) * (tiles / 8) + b / 8 : b;
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    const int t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const int wm = wave / 2, wn = wave % 2;
+    const int fr = lane % 32, h = lane / 32;
+    const int nk = K / 64;
 
-    uint4 xreg[4], wreg[2];
-    auto gload = [&](int k0) {
+    const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
+    const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
+
+    // Source offsets (k = 0) of this lane in each of the wave's DMA units,
+    // swizzled so LDS chunk s of row r holds global chunk s ^ f(r).
+    uint32_t xoff[XUW], woff[WUW];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int row = m0 + xr + 32 * p;
-            xreg[p] = row < M ? *reinterpret_cast<const uint4 *>(X + (size_t)row * K + k0 + xc) : make_uint4(0, 0, 0, 0);
-        }
+    for (int q = 0; q < XUW; ++q) {
+        const int row = (wave * XUW + q) * 8 + lane / 8, s = lane % 8;
+        xoff[q] = ((uint32_t)row * K + (uint32_t)(s ^ ((row >> 1) & 7)) * 8) * 2u;
+    }
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int row = n0 + wr + 64 * p;
-            wreg[p] = row < N ? *reinterpret_cast<const uint4 *>(W + (size_t)row * K + k0 + wc) : make_uint4(0, 0, 0, 0);
-        }
+    for (int q = 0; q < WUW; ++q) {
+        const int row = (wave * WUW + q) * 16 + lane / 4, s = lane % 4;
+        woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 2) & 3)) * 16;
+    }
+    auto dma = [&](Stage<BM, BN> &st, int kt) {
+        const bool live = kt < nk;
+#pragma unroll
+        for (int q = 0; q < XUW; ++q) dma16(rx, st.x + (wave * XUW + q) * 1024, live ? xoff[q] + kt * 128 : kOOB);
+#pragma unroll
+        for (int q = 0; q < WUW; ++q) dma16(rw, st.w + (wave * WUW + q) * 1024, live ? woff[q] + kt * 64 : kOOB);
     };
-    auto lstore = [&](int buf) {
-        uint8_t *xs = lds + buf * (XS_BYTES + WS_BYTES);
-        uint8_t *ws = xs + XS_BYTES;
+
+    floatx16 acc[FN][FM];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) *reinterpret_cast<uint4 *>(xs + (xr + 32 * p) * XS_STRIDE + xc * 2) = xreg[p];
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            // W rows are 72 B apart: 8-byte aligned only, store as two halves.
-            uint2 *d = reinterpret_cast<uint2 *>(ws + (wr + 64 * p) * WS_STRIDE + wc);
-            d[0] = make_uint2(wreg[p].x, wreg[p].y);
-            d[1] = make_uint2(wreg[p].z, wreg[p].w);
-        }
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // A k-step's fragments: raw int8 W (expanded just before the MFMA) and fp16 X.
+    struct Frag {
+        uint2 w[4][FN];
+        half8 x[4][FM];
     };
-
-    floatx4 acc[4][4];
+    auto fetch = [&](const Stage<BM, BN> &st, Frag &f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int k16 = 0; k16 < 4; ++k16) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int nk = K / BK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    const int fr = lane % 16;        // operand row within a 16-row tile
-    const int fk = (lane / 16) * 8;  // first of the lane's 8 k values within a 32-k step
-
-#pragma unroll 1
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
-        const uint8_t *xs = lds + buf * (XS_BYTES + WS_BYTES);
-        const uint8_t *ws = xs + XS_BYTES;
-#pragma unroll
-        for (int ks = 0; ks < BK; ks += 32) {
-            half8 a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint2 wv = *reinterpret_cast<const uint2 *>(ws + (wn * 64 + i * 16 + fr) * WS_STRIDE + ks + fk);
-                a[i] = i8x8_to_half8(wv);
+            for (int i = 0; i < FN; ++i) {
+                const int r = wn * TN + i * 32 + fr;
+                f.w[k16][i] = *reinterpret_cast<const uint2 *>(st.w + r * 64 + ((k16 ^ ((r >> 2) & 3)) * 16) + h * 8);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                b[j] = *reinterpret_cast<const half8 *>(xs + (wm * 64 + j * 16 + fr) * XS_STRIDE + (ks + fk) * 2);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FM; ++j) {
+                const int r = wm * TM + j * 32 + fr, c = 2 * k16 + h;
+                f.x[k16][j] = *reinterpret_cast<const half8 *>(st.x + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+            }
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
+    };
+    auto mma = [&](const Frag &f) {
+#pragma unroll
+        for (int k16 = 0; k16 < 4; ++k16) {
+            half8 a[FN];
+#pragma unroll
+            for (int i = 0; i < FN; ++i) a[i] = i8x8_to_half8(f.w[k16][i]);
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], f.x[k16][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // Wait until this wave's DMA for the step about to be read has landed
+    // (later steps may stay in flight), then let every wave see every unit.
+    auto ready = [&](int n_later) {
+        if (n_later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_le(2 * NOUT));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_le(NOUT));
         __syncthreads();
-    }
+    };
 
-    // Epilogue: acc[i][j] holds D[feature = 4*(lane/16) + r][token = lane%16]
-    // of tile (features n0 + wn*64 + 16 i, tokens m0 + wm*64 + 16 j).
+    if constexpr (PINGPONG) {
+        // Iteration on step k: step k+1 is ready, step k's stage is free (its
+        // fragments are in registers), so DMA(k+3) refills it while the
+        // fragments of k+1 are read and the MFMAs of k run.
+        Frag fa, fb;
+        dma(s0, 0);
+        dma(s1, 1);
+        dma(s2, 2);
+        ready(2);
+        fetch(s0, fa);
+#pragma unroll 1
+        for (int kt = 0; kt < nk; kt += 6) {
+            ready(1); dma(s0, kt + 3); fetch(s1, fb); mma(fa);
+            ready(1); dma(s1, kt + 4); fetch(s2, fa); mma(fb);
+            ready(1); dma(s2, kt + 5); fetch(s0, fb); mma(fa);
+            ready(1); dma(s0, kt + 6); fetch(s1, fa); mma(fb);
+            ready(1); dma(s1, kt + 7); fetch(s2, fb); mma(fa);
+            ready(1); dma(s2, kt + 8); fetch(s0, fa); mma(fb);
+        }
+    } else {
+        Frag f;
+        dma(s0, 0);
+        dma(s1, 1);
+#pragma unroll 1
+        for (int kt = 0; kt < nk; kt += 3) {
+            ready(1); dma(s2, kt + 2); fetch(s0, f); mma(f);
+            ready(1); dma(s0, kt + 3); fetch(s1, f); mma(f);
+            ready(1); dma(s1, kt + 4); fetch(s2, f); mma(f);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));  // no DMA in flight past this point
+
+    // Epilogue: acc[i][j][r] = D[feature 8*(r/4) + 4*(lane/32) + r%4][token lane%32]
+    // of tile (features n0 + wn*TN + 32 i, tokens m0 + wm*TM + 32 j).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int nb = n0 + wn * 64 + i * 16 + (lane / 16) * 4;
-        float sc[4];
+    for (int i = 0; i < FN; ++i) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? scales[nb + r] : 0.0f;
+        for (int g = 0; g < 4; ++g) {
+            const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;
+            float sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int mm = m0 + wm * 64 + j * 16 + fr;
-            if (mm >= M) continue;
-            float v[4];
+            for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? scales[nb + r] : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * sc[r];
-            const size_t o = (size_t)mm * N + nb;
-            if (nb + 4 <= N && (N % 4) == 0) {
-                if (y_f16) {
-                    h2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
-                    uint2 pk = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-                    *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yv) + o) = pk;
+            for (int j = 0; j < FM; ++j) {
+                const int mm = m0 + wm * TM + j * 32 + fr;
+                if (mm >= M) continue;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r];
+                const size_t o = (size_t)mm * N + nb;
+                if (nb + 4 <= N && (N % 4) == 0) {
+                    if (y_f16) {
+                        const h2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yv) + o) =
+                            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                    } else {
+                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yv) + o) =
+                            make_float4(v[0], v[1], v[2], v[3]);
+                    }
                 } else {
-                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yv) + o) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (nb + r >= N) break;
-                    if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o + r] = (_Float16)v[r];
-                    else reinterpret_cast<float *>(Yv)[o + r] = v[r];
+                    for (int r = 0; r < 4; ++r) {
+                        if (nb + r >= N) break;
+                        if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o + r] = (_Float16)v[r];
+                        else reinterpret_cast<float *>(Yv)[o + r] = v[r];
+                    }
                 }
             }
         }
     }
+}
+
+template <int BM, int BN, bool PINGPONG>
+int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, hipStream_t s) {
+    const int64_t N = w.n_out, K = w.k_in;
+    const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
+    const int64_t tiles = (int64_t)tiles_m * tiles_n;
+    if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG>), dim3((unsigned)tiles), dim3(TH), 0, s,
+                       (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m,
+                       (int)N, (int)K, tiles_m, tiles_n);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
 }
 
 }  // namespace
@@ -178,15 +279,14 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
                 hipStream_t s) {
     (void)num_cus;
     const int64_t N = w.n_out, K = w.k_in;
-    if (w.format != RQ_Q_ROWWISE_I8 || xt != RQ_F16 || K % BK != 0 || !aligned(w.codes, 16) || !aligned(x, 16) ||
-        m > 0x7fffffff || N > 0x7fffffff || cdiv(m, BM) > 65535)
+    // 32-bit buffer offsets: a 256-row panel of X (256 * K * 2 bytes) must stay below 2^31.
+    if (w.format != RQ_Q_ROWWISE_I8 || xt != RQ_F16 || K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) ||
+        !aligned(x, 16) || m > 0x7fffffff || N > 0x7fffffff)
         return RQ_ERR_UNSUPPORTED;
     if (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)) return RQ_ERR_UNSUPPORTED;
-    const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(m, BM));
-    hipLaunchKernelGGL(k_gemm_rowwise, grid, dim3(TH), 0, s, (const int8_t *)w.codes, w.scales,
-                       (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K);
-    RQ_LAUNCH_CHECK();
-    return RQ_OK;
+    if (m <= 64) return launch_tiled<64, 128, false>(w, x, y, yt, m, s);
+    if (m < 1024) return launch_tiled<128, 128, false>(w, x, y, yt, m, s);
+    return launch_tiled<256, 128, true>(w, x, y, yt, m, s);
 }
 
 }  // namespace rq
