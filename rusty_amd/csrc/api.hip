@@ -281,6 +281,8 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
     if (w->k_in > 0) {
         st = RQ_ERR_UNSUPPORTED;
         if (m <= 4 && x_dtype == RQ_F16) st = launch_gemv_decode(*w, x, y, y_dtype, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 16 && x_dtype == RQ_F16)
+            st = launch_gemv_mfma(*w, x, y, y_dtype, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(*w, x, x_dtype, y, y_dtype, (int)m, ctx->num_cus, s);
         if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(*w, x, x_dtype, y, y_dtype, m, ctx->num_cus, s);
         if (st != RQ_ERR_UNSUPPORTED) return st;

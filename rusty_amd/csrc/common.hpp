@@ -39,6 +39,7 @@ int launch_rowwise_dequantize(const int8_t *q, const float *scales, float *out, 
 int launch_matmul_f32(int variant, const float *a, const float *b, float *out, int64_t m, int64_t k,
                       int64_t n, hipStream_t s);
 int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
+int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
 int launch_gemv(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m,
                 int num_cus, hipStream_t s);
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,

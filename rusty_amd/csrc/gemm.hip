@@ -63,9 +63,15 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void *lds_
                  : "memory", "m0");
 }
 
-// s_waitcnt immediate for "at most n vector-memory operations outstanding"
-// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14]).
-constexpr int vmcnt_le(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+// Waits until at most N vector-memory operations of this wave are outstanding
+// (they retire in issue order).  Inline asm with a memory clobber, so the
+// compiler cannot move LDS reads of the landed data above the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until every LDS read of this wave has returned its data.
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t u, uint32_t sel) {
     const uint32_t m = __builtin_amdgcn_perm(0x64646464u, u, sel);
@@ -181,8 +187,8 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
     // Wait until this wave's DMA for the step about to be read has landed
     // (later steps may stay in flight), then let every wave see every unit.
     auto ready = [&](int n_later) {
-        if (n_later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_le(2 * NOUT));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_le(NOUT));
+        if (n_later == 2) wait_vmcnt<2 * NOUT>();
+        else wait_vmcnt<NOUT>();
         __syncthreads();
     };
 
@@ -216,7 +222,7 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
             ready(1); dma(s1, kt + 4); fetch(s2, f); mma(f);
         }
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));  // no DMA in flight past this point
+    wait_vmcnt<0>();  // no DMA in flight past this point
 
     // Epilogue: acc[i][j][r] = D[feature 8*(r/4) + 4*(lane/32) + r%4][token lane%32]
     // of tile (features n0 + wn*TN + 32 i, tokens m0 + wm*TM + 32 j).
