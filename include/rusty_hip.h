@@ -152,6 +152,17 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y,
                rq_dtype y_dtype, int64_t m, rq_stream stream);
 
+/* MLP::forward (rusty-graph/src/lib.rs:317-323):
+ * y = down( silu(x . gate^T) * (x . up^T) ), silu(v) = v / (1 + exp(-v))
+ * (kernels.wgsl:104-113; the elementwise product kernels.wgsl:146-151).
+ * gate, up: [I, H]; down: [H, I]; x [m, H]; y [m, H].
+ * h: caller workspace of 2*m*I fp16 values; on return its first m*I hold the
+ * activated intermediate silu(g)*u (rounded to fp16).  For m <= 16 with fp16
+ * activations and per-row int8 weights, gate and up are read in one fused
+ * pass with the silu*mul epilogue. */
+int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
+                  rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

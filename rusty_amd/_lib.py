@@ -65,6 +65,8 @@ _SIGNATURES = {
     "rq_matmul_bt": [_P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
     "rq_matmul_at": [_P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
     "rq_qmatmul": [_P, POINTER(rq_qweight), _P, c_int, _P, c_int, c_int64, _P],
+    "rq_mlp_swiglu": [_P, POINTER(rq_qweight), POINTER(rq_qweight), POINTER(rq_qweight), _P, c_int, _P, _P, c_int,
+                      c_int64, _P],
 }
 _RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p}
 

@@ -265,6 +265,26 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
     return matmul_common(ctx, MM_ATB, a, b, out, m, k, n, stream);
 }
 
+}  // extern "C"
+
+// Fused linear dispatch (arguments already validated): decode kernels for
+// few tokens, the MFMA GEMM for many, the generic kernel for anything the
+// tuned paths do not serve.
+static int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
+                            int64_t m, hipStream_t s) {
+    if (w.k_in > 0) {
+        int st = RQ_ERR_UNSUPPORTED;
+        if (m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 16 && xt == RQ_F16) st = launch_gemv_mfma(w, x, y, yt, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(w, x, xt, y, yt, (int)m, ctx->num_cus, s);
+        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, s);
+        if (st != RQ_ERR_UNSUPPORTED) return st;
+    }
+    return launch_qlinear_generic(w, x, xt, y, yt, m, s);
+}
+
+extern "C" {
+
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y, rq_dtype y_dtype,
                int64_t m, rq_stream stream) {
     RQ_ENTER(ctx);
@@ -277,17 +297,43 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
     if (!mul_ok(m, w->k_in, &t) || !mul_ok(m, w->n_out, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
     if (m == 0 || w->n_out == 0) return RQ_OK;
     if (!y || (w->k_in > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
+    return qmatmul_dispatch(ctx, *w, x, x_dtype, y, y_dtype, m, pick(ctx, stream));
+}
+
+int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
+                  rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st;
+    if ((st = check_qweight(gate)) != RQ_OK || (st = check_qweight(up)) != RQ_OK || (st = check_qweight(down)) != RQ_OK)
+        return st;
+    if ((x_dtype != RQ_F16 && x_dtype != RQ_F32) || (y_dtype != RQ_F16 && y_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    const int64_t I = gate->n_out, H = gate->k_in;
+    if (up->n_out != I || up->k_in != H || down->n_out != H || down->k_in != I)
+        return fail(RQ_ERR_SHAPE, "SwiGLU shapes: gate/up [%lld,%lld], down must be [%lld,%lld]", (long long)I,
+                    (long long)H, (long long)H, (long long)I);
+    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
+    int64_t t;
+    if (!mul_ok(m, 2 * I, &t) || !mul_ok(m, H, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0 || H == 0) return RQ_OK;
+    if (!y || !h || (H > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation or workspace pointer");
     hipStream_t s = pick(ctx, stream);
-    if (w->k_in > 0) {
-        st = RQ_ERR_UNSUPPORTED;
-        if (m <= 4 && x_dtype == RQ_F16) st = launch_gemv_decode(*w, x, y, y_dtype, (int)m, s);
-        if (st == RQ_ERR_UNSUPPORTED && m <= 16 && x_dtype == RQ_F16)
-            st = launch_gemv_mfma(*w, x, y, y_dtype, (int)m, s);
-        if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(*w, x, x_dtype, y, y_dtype, (int)m, ctx->num_cus, s);
-        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(*w, x, x_dtype, y, y_dtype, m, ctx->num_cus, s);
-        if (st != RQ_ERR_UNSUPPORTED) return st;
+    // gate/up pass -> h (fp16, [m, I])
+    st = RQ_ERR_UNSUPPORTED;
+    if (x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 16) st = launch_swiglu_mfma(*gate, *up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m > 16) {
+        // prefill: gate and up through the GEMM into the two halves of the
+        // workspace, then h = silu(g) * u in place over the first half
+        _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
+        st = launch_gemm(*gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, s);
+        if (st == RQ_OK) st = launch_gemm(*up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, s);
+        if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
     }
-    return launch_qlinear_generic(*w, x, x_dtype, y, y_dtype, m, s);
+    if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(*gate, *up, x, x_dtype, h, m, s);
+    if (st != RQ_OK) return st;
+    // down projection of h
+    return qmatmul_dispatch(ctx, *down, h, RQ_F16, y, y_dtype, m, s);
 }
 
 }  // extern "C"

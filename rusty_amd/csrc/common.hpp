@@ -46,6 +46,11 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
                 int num_cus, hipStream_t s);
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                            int64_t m, hipStream_t s);
+int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
+int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
+int launch_swiglu_generic(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h,
+                          int64_t m, hipStream_t s);
+int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_t s);
 
 enum MatmulVariant { MM_AB = 0, MM_ABT = 1, MM_ATB = 2 };
 

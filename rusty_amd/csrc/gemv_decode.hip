@@ -67,17 +67,25 @@ __device__ __forceinline__ float wave_total(float v) {
     return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
 }
 
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
 // M: activation rows (m_act <= M); CPT: chunks per thread; TPR: threads per
 // row group; R: rows per row group; FMT: 0 = ROWWISE_I8, 1 = AFFINE_U8.
-template <int M, int CPT, int TPR, int R, int FMT>
+// SWI: SwiGLU gate/up pass (rowwise only) -- W/scales are the gate weight,
+// W2/scales2 the up weight of the same shape; the block loads R gate rows and
+// the same R up rows per row group and writes h = silu(g) * u (fp16).
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
+                                                    const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                     const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                     int y_f16, int m_act, int N, int K, int group) {
+    static_assert(!SWI || FMT == 0, "SwiGLU pass is rowwise only");
     constexpr int RP = DT / TPR;
     constexpr int ROWS = R * RP;
     constexpr int TASKS = ROWS * M;
-    __shared__ float part[TASKS][TPR];
+    constexpr int NR = SWI ? 2 * R : R;  // weight rows loaded per row group
+    __shared__ float part[SWI ? 2 * TASKS : TASKS][TPR];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int rp = t / TPR, tt = t % TPR;
@@ -101,14 +109,15 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     // Weight chunks: R rows x CPT chunks per thread, all in flight.
     const int rows_here = min(ROWS, N - row0);
     const auto rw = make_rsrc(W + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
-    uint4 w[R][CPT];
+    const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
+    uint4 w[NR][CPT];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int c = tt + TPR * j;
-            const uint32_t off = c < C ? (uint32_t)(r * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
-            w[r][j] = bload<2>(rw, off);
+            const uint32_t off = c < C ? (uint32_t)((r % R) * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
+            w[r][j] = bload<2>(r < R ? rw : rw2, off);
         }
     float sg[R][CPT], bg[R][CPT];
     if constexpr (FMT == 1) {
@@ -143,7 +152,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
         }
 
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < NR; ++r) {
         float p[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) p[m] = 0.0f;
@@ -177,21 +186,28 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const float v = FMT == 0 ? __builtin_fmaf(-1152.0f, xs_tot[m], p[m]) : p[m];
-            part[(r * RP + rp) * M + m][tt] = v;
+            // up rows (r >= R) land TASKS entries after their gate rows
+            part[(r / R) * TASKS + ((r % R) * RP + rp) * M + m][tt] = v;
         }
     }
     __syncthreads();
 
     // Each wave finishes whole (row, token) tasks.
     for (int task = wave; task < TASKS; task += DT / 64) {
-        float v = 0.0f;
+        float v = 0.0f, v2 = 0.0f;
 #pragma unroll
         for (int i = 0; i < TPR / 64; ++i) v += part[task][lane + 64 * i];
+        if constexpr (SWI) {
+#pragma unroll
+            for (int i = 0; i < TPR / 64; ++i) v2 += part[TASKS + task][lane + 64 * i];
+        }
         const float tot = wave_total(v);
+        const float tot2 = SWI ? wave_total(v2) : 0.0f;
         const int rin = task / M, m = task % M;
         const int row = row0 + rin;
         if (lane == 0 && rin < rows_here && m < m_act) {
-            const float y = FMT == 0 ? tot * scales[row] : tot;
+            float y = FMT == 0 ? tot * scales[row] : tot;
+            if constexpr (SWI) y = silu(y) * (tot2 * scales2[row]);
             const size_t o = (size_t)m * N + row;
             if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
             else reinterpret_cast<float *>(Yv)[o] = y;
@@ -199,13 +215,16 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     }
 }
 
-using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const _Float16 *, void *, int, int, int, int,
-                          int);
+using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
+                          const _Float16 *, void *, int, int, int, int, int);
 
+// fmt 2 selects the SwiGLU gate/up pass.  Rows per row group: 2 at m = 1,
+// else 4 (SwiGLU: pairs, so the same number of weight bytes per block).
 template <int M, int CPT, int TPR>
 DecodeFn pick_fmt(int fmt) {
     constexpr int R = M == 1 ? 2 : 4;
-    return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, R, 0> : &k_gemv_decode<M, CPT, TPR, R, 1>;
+    if (fmt == 2) return &k_gemv_decode<M, CPT, TPR, R / 2, 0, true>;
+    return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, R, 0, false> : &k_gemv_decode<M, CPT, TPR, R, 1, false>;
 }
 
 template <int M, int CPT>
@@ -229,23 +248,36 @@ DecodeFn pick_cpt(int cpt, int tpr, int fmt) {
 
 }  // namespace
 
-int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
+static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, void *y, rq_dtype yt, int m,
+                         hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
         !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && w.group % 16 != 0))
+        return RQ_ERR_UNSUPPORTED;
+    if (w2 && (w.format != RQ_Q_ROWWISE_I8 || w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16)))
         return RQ_ERR_UNSUPPORTED;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
     const int cpt = (int)cdiv(C, tpr);
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
-    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, w.format) : mt == 2 ? pick_cpt<2>(cpt, tpr, w.format)
-                                                                       : pick_cpt<4>(cpt, tpr, w.format);
-    const int rows = (mt == 1 ? 2 : 4) * (DT / tpr);
+    const int fmt = w2 ? 2 : w.format;
+    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt) : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt)
+                                                                 : pick_cpt<4>(cpt, tpr, fmt);
+    const int rows = (mt == 1 ? 2 : 4) / (w2 ? 2 : 1) * (DT / tpr);
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
-                       (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.group);
+                       w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, (const _Float16 *)x, y,
+                       yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.group);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
+}
+
+int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
+    return launch_decode(w, nullptr, x, y, yt, m, s);
+}
+
+int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s) {
+    return launch_decode(gate, &up, x, h, RQ_F16, m, s);
 }
 
 }  // namespace rq

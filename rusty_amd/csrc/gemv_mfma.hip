@@ -80,16 +80,24 @@ struct StepBuf {
     uint8_t x[XSTEP];
 };
 
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// SWI: SwiGLU gate/up pass -- the block's 16 weight rows are 8 gate rows (W)
+// and the same 8 rows of the up weight (W2); it writes h = silu(g) * u (fp16).
+template <bool SWI>
 __global__ __launch_bounds__(TH) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
+                                                  const int8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                   const _Float16 *__restrict__ X, void *__restrict__ Yv, int y_f16,
                                                   int m_act, int N, int K) {
+    constexpr int RB = SWI ? FB / 2 : FB;  // output rows per block
     __shared__ __attribute__((aligned(1024))) StepBuf ring[4][RING];  // [wave][slot]
     __shared__ floatx4 red[4][64];
 
     const int t = threadIdx.x, wave = t / 64, lane = t % 64;
-    const int n0 = blockIdx.x * FB;
-    const int rows_here = min(FB, N - n0);
+    const int n0 = blockIdx.x * RB;
+    const int rows_here = min(RB, N - n0);
     const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
+    const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
     const int nsteps_total = (K + KS - 1) / KS;
     const int my_steps = (nsteps_total - wave + 3) / 4;  // steps wave, wave + 4, ...
@@ -106,7 +114,9 @@ __global__ __launch_bounds__(TH) void k_gemv_mfma(const int8_t *__restrict__ W, 
         for (int u = 0; u < WSTEP / 1024; ++u) {
             const int row = 4 * u + lane / 16, c = lane % 16;
             const int k = k0 + ((c ^ row) & 15) * 16;
-            dma16(rw, b.w + u * 1024, (live && k < K) ? (uint32_t)row * K + k : kOOB);
+            const bool second = SWI && u >= WSTEP / 2048;  // SwiGLU: rows 8..15 come from the up weight
+            const uint32_t grow = SWI ? (uint32_t)(row % RB) : (uint32_t)row;
+            dma16(second ? rw2 : rw, b.w + u * 1024, (live && k < K) ? grow * K + k : kOOB);
         }
 #pragma unroll
         for (int u = 0; u < XSTEP / 1024; ++u) {
@@ -164,7 +174,22 @@ __global__ __launch_bounds__(TH) void k_gemv_mfma(const int8_t *__restrict__ W, 
             v[3] += o[3];
         }
         const int m = fr;
-        if (m < m_act) {
+        if constexpr (SWI) {
+            // gate rows 0..7 sit in lane groups 0-1, up rows 8..15 in groups 2-3
+            red[0][lane] = v;
+            wait_lgkm0();
+            const floatx4 u = red[0][(lane + 32) % 64];
+            if (g < 2 && m < m_act) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 4 * g + r;
+                    if (f < rows_here) {
+                        const float h = silu(v[r] * scales[n0 + f]) * (u[r] * scales2[n0 + f]);
+                        reinterpret_cast<_Float16 *>(Yv)[(size_t)m * N + n0 + f] = (_Float16)h;
+                    }
+                }
+            }
+        } else if (m < m_act) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int f = 4 * g + r;
@@ -181,17 +206,33 @@ __global__ __launch_bounds__(TH) void k_gemv_mfma(const int8_t *__restrict__ W, 
 
 }  // namespace
 
-int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
+static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x, void *y, rq_dtype yt, int m,
+                       hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     // 32-bit buffer offsets: 16 activation rows of K fp16 must stay below 2^31 bytes.
     if (w.format != RQ_Q_ROWWISE_I8 || m < 1 || m > 16 || K % 16 != 0 || K > (1 << 24) || N > 0x7fffffff ||
         !aligned(w.codes, 16) || !aligned(x, 16))
         return RQ_ERR_UNSUPPORTED;
-    const int64_t blocks = cdiv(N, FB);
-    hipLaunchKernelGGL(k_gemv_mfma, dim3((unsigned)blocks), dim3(TH), 0, s, (const int8_t *)w.codes, w.scales,
-                       (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K);
+    if (w2 && (w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16))) return RQ_ERR_UNSUPPORTED;
+    const int64_t blocks = cdiv(N, w2 ? FB / 2 : FB);
+    if (w2)
+        hipLaunchKernelGGL(k_gemv_mfma<true>, dim3((unsigned)blocks), dim3(TH), 0, s, (const int8_t *)w.codes,
+                           w.scales, (const int8_t *)w2->codes, w2->scales, (const _Float16 *)x, y, 1, m, (int)N,
+                           (int)K);
+    else
+        hipLaunchKernelGGL(k_gemv_mfma<false>, dim3((unsigned)blocks), dim3(TH), 0, s, (const int8_t *)w.codes,
+                           w.scales, nullptr, nullptr, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, m, (int)N,
+                           (int)K);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
+}
+
+int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
+    return launch_mfma(w, nullptr, x, y, yt, m, s);
+}
+
+int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s) {
+    return launch_mfma(gate, &up, x, h, RQ_F16, m, s);
 }
 
 }  // namespace rq

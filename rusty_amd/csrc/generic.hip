@@ -55,7 +55,84 @@ __global__ __launch_bounds__(TH) void k_qlinear_generic(const uint8_t *__restric
     }
 }
 
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float deq(const uint8_t *codes, const float *scales, const float *biases, int fmt,
+                                     int64_t group, int64_t n, int64_t k, int64_t K) {
+    if (fmt == RQ_Q_ROWWISE_I8) return (float)(int8_t)codes[n * K + k];
+    {
+#pragma clang fp contract(off)
+        const int64_t g = (n * K + k) / group;
+        const float p = (float)codes[n * K + k] * scales[g];
+        return p + (biases ? biases[g] : 0.0f);
+    }
+}
+
+// SwiGLU gate/up pass for any shape, format and activation dtype: one block
+// per intermediate feature i, h[m, i] = silu(x.gate[i]) * (x.up[i]) in fp16.
+__global__ __launch_bounds__(TH) void k_swiglu_generic(rq_qweight gate, rq_qweight up, const void *__restrict__ X,
+                                                       int x_f16, _Float16 *__restrict__ H, int64_t M) {
+    __shared__ float red[2][TH / 64];
+    const int64_t i = blockIdx.x, K = gate.k_in, I = gate.n_out;
+    const int t = threadIdx.x;
+    const int64_t gg = gate.group > 0 ? gate.group : 1, gu = up.group > 0 ? up.group : 1;
+    for (int64_t m = 0; m < M; ++m) {
+        float ag = 0.0f, au = 0.0f;
+        for (int64_t k = t; k < K; k += TH) {
+            const float x = x_f16 ? ld<_Float16>(X, m * K + k) : ld<float>(X, m * K + k);
+            ag = __builtin_fmaf(deq((const uint8_t *)gate.codes, gate.scales, gate.biases, gate.format, gg, i, k, K), x, ag);
+            au = __builtin_fmaf(deq((const uint8_t *)up.codes, up.scales, up.biases, up.format, gu, i, k, K), x, au);
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            ag += __shfl_xor(ag, o, 64);
+            au += __shfl_xor(au, o, 64);
+        }
+        if (t % 64 == 0) {
+            red[0][t / 64] = ag;
+            red[1][t / 64] = au;
+        }
+        __syncthreads();
+        if (t == 0) {
+            float g = 0.0f, u = 0.0f;
+            for (int w = 0; w < TH / 64; ++w) {
+                g += red[0][w];
+                u += red[1][w];
+            }
+            if (gate.format == RQ_Q_ROWWISE_I8) g *= gate.scales[i];
+            if (up.format == RQ_Q_ROWWISE_I8) u *= up.scales[i];
+            H[m * I + i] = (_Float16)(silu(g) * u);
+        }
+        __syncthreads();
+    }
+}
+
+// h = silu(g) * u elementwise on fp16 (the prefill SwiGLU epilogue).
+__global__ __launch_bounds__(TH) void k_silu_mul(const _Float16 *__restrict__ G, const _Float16 *__restrict__ U,
+                                                 _Float16 *__restrict__ H, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * TH + threadIdx.x; i < n; i += (int64_t)gridDim.x * TH)
+        H[i] = (_Float16)(silu((float)G[i]) * (float)U[i]);
+}
+
 }  // namespace
+
+int launch_swiglu_generic(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
+                          hipStream_t s) {
+    if (gate.n_out > 0x7fffffff) return fail(RQ_ERR_SHAPE, "intermediate size too large for the generic kernel");
+    hipLaunchKernelGGL(k_swiglu_generic, dim3((unsigned)gate.n_out), dim3(TH), 0, s, gate, up, x, xt == RQ_F16 ? 1 : 0,
+                       (_Float16 *)h, m);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_t s) {
+    int64_t blocks = cdiv(n, TH);
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) return RQ_OK;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)blocks), dim3(TH), 0, s, (const _Float16 *)g, (const _Float16 *)u,
+                       (_Float16 *)h, n);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
 
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
                            hipStream_t s) {

@@ -301,3 +301,21 @@ class ComputeEngine:
         d = w.descriptor()
         call("rq_qmatmul", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], out.ptr, _XDT[out.dtype], m,
              _stream(stream))
+
+    def mlp_swiglu(self, ctx: WgpuContext, x: UnifiedTensor, gate: QuantizedTensor, up: QuantizedTensor,
+                   down: QuantizedTensor, out: UnifiedTensor, h: UnifiedTensor | None = None,
+                   stream=None) -> UnifiedTensor:
+        """``MLP::forward`` (rusty-graph/src/lib.rs:317-323):
+        ``out = down(silu(x . gate^T) * (x . up^T))``.  ``h`` is the fp16
+        workspace (2 * m * I values); returned, its first m*I hold silu(g)*u."""
+        m = x.numel // gate.k_in
+        if h is None:
+            h = UnifiedTensor.empty(ctx, [2, m, gate.n_out], DType.FP16)
+        if h.dtype is not DType.FP16 or h.numel < 2 * m * gate.n_out:
+            raise ValueError("h must be an fp16 workspace of 2*m*I values")
+        if out.numel != m * down.n_out:
+            raise ValueError("out does not match [m, H]")
+        dg, du, dd = gate.descriptor(), up.descriptor(), down.descriptor()
+        call("rq_mlp_swiglu", ctx.handle, ctypes.byref(dg), ctypes.byref(du), ctypes.byref(dd), x.ptr,
+             _XDT[x.dtype], h.ptr, out.ptr, _XDT[out.dtype], m, _stream(stream))
+        return h

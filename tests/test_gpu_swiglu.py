@@ -1,0 +1,110 @@
+"""GPU parity of the SwiGLU MLP (rq_mlp_swiglu) against the oracle.
+
+Reference: MLP::forward, rusty-graph/src/lib.rs:317-323 --
+y = down( silu(x . gate^T) * (x . up^T) ), silu from kernels.wgsl:104-113.
+The truth (oracle/oracle.c orc_swiglu_truth) is computed in f64 from the same
+fp16 activations and exactly dequantized weights, with the intermediate h
+rounded to fp16 as the device stores it.  Tolerance (fp16 outputs):
+|dy| <= 2e-3*|y| + 2e-3*max|y| elementwise; h is checked the same way.
+"""
+import numpy as np
+import pytest
+
+from conftest import f16_tol_check
+from oracle import oracle as orc
+from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float16):
+    G = QuantizedTensor.rowwise(ctx, wg, sg)
+    U = QuantizedTensor.rowwise(ctx, wu, su)
+    D = QuantizedTensor.rowwise(ctx, wd, sd)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16 if x.dtype == np.float16 else DType.FP32)
+    Y = UnifiedTensor.new(ctx, np.full((x.shape[0], wd.shape[0]), np.nan, ydt),
+                          dtype=DType.FP16 if ydt is np.float16 else DType.FP32)
+    h = engine.mlp_swiglu(ctx, X, G, U, D, Y)
+    m, inter = x.shape[0], wg.shape[0]
+    return Y.to_vec(), h.to_vec().reshape(-1)[: m * inter].reshape(m, inter)
+
+
+def h_truth(x, wg, sg, wu, su):
+    g = orc.qlinear_truth(wg, sg, None, x.astype(np.float32), 0)
+    u = orc.qlinear_truth(wu, su, None, x.astype(np.float32), 0)
+    with np.errstate(over="ignore"):
+        return (g / (1.0 + np.exp(-g)) * u).astype(np.float16).astype(np.float64)
+
+
+def weights(g, inter, hidden):
+    wg, sg = synth.rowwise_weight(g, inter, hidden)
+    wu, su = synth.rowwise_weight(g, inter, hidden)
+    wd, sd = synth.rowwise_weight(g, hidden, inter)
+    return wg, sg, wu, su, wd, sd
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16])
+def test_swiglu_small(ctx, engine, m):
+    g = synth.rng(300 + m)
+    wg, sg, wu, su, wd, sd = weights(g, 200, 1024)  # 200: ragged for every row-batch size
+    x = synth.activations(g, m, 1024)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd)
+    _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
+    assert ok_h, "intermediate h"
+    truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32))
+    max_abs, rel, ok = f16_tol_check(y, truth)
+    print(f"[swiglu m={m}] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_config3_swiglu_7b(ctx, engine, m):
+    # configs[2] statistics (X ~ N(0,1), scales up to 0.02, K = 11008) put |y|
+    # near 1e5, past the fp16 range: y is produced in f32 here, h stays fp16
+    # (|h| < 65504 at these statistics; checked below).
+    g = synth.rng(3000 + m)
+    wg, sg, wu, su, wd, sd = weights(g, 11008, 4096)
+    x = synth.activations(g, m, 4096)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    ht = h_truth(x, wg, sg, wu, su)
+    assert np.isfinite(ht).all() and np.isfinite(h).all()
+    _, _, ok_h = f16_tol_check(h, ht)
+    assert ok_h
+    truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32))
+    max_abs, rel, ok = f16_tol_check(y, truth)
+    print(f"[C3 swiglu m={m}] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
+def test_swiglu_prefill_path(ctx, engine):
+    g = synth.rng(77)
+    wg, sg, wu, su, wd, sd = weights(g, 384, 512)
+    x = synth.activations(g, 130, 512)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd)
+    # prefill rounds g and u to fp16 before silu*mul: same tolerance
+    _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
+    assert ok_h
+    _, _, ok = f16_tol_check(y, orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32)))
+    assert ok
+
+
+def test_swiglu_generic_paths(ctx, engine):
+    g = synth.rng(78)
+    wg, sg, wu, su, wd, sd = weights(g, 96, 100)  # K % 16 != 0: generic gate/up and down kernels
+    x = synth.activations(g, 3, 100, dtype=np.float32)  # f32 activations
+    y, _ = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    _, _, ok = f16_tol_check(y, orc.swiglu_truth(wg, sg, wu, su, wd, sd, x))
+    assert ok
+
+
+def test_swiglu_shape_error(ctx, engine):
+    from rusty_amd import RqError
+
+    g = synth.rng(1)
+    wg, sg, wu, su, wd, sd = weights(g, 32, 64)
+    G, U = QuantizedTensor.rowwise(ctx, wg, sg), QuantizedTensor.rowwise(ctx, wu, su)
+    Dbad = QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, 64, 16))  # down must be [64, 32]
+    X = UnifiedTensor.new(ctx, synth.activations(g, 1, 64), dtype=DType.FP16)
+    Y = UnifiedTensor.empty(ctx, [1, 64], DType.FP16)
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        engine.mlp_swiglu(ctx, X, G, U, Dbad, Y)
