@@ -163,6 +163,72 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
 int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
                   rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream);
 
+/* ---- int8-weight Llama greedy decode ------------------------------------
+ * LlamaModel::forward (rusty-graph/src/lib.rs:420-436) over LlamaBlock
+ * (:364-378: norm1 -> Attention -> add -> norm2 -> MLP -> add), Attention
+ * with RoPE and a KV cache (:191-283; KVCacheLayer :473-478), RMSNorm
+ * (kernels.wgsl:87-102, every row), greedy top_k with k = 1
+ * (kernels.wgsl:173-188) and the embedding gather (lib.rs:121-135) on the
+ * device.  The reference has no decode loop; this runner defines it: each
+ * step is one HIP graph launch, with the position, the token sequence and the
+ * KV cache in device memory.  Weights are borrowed (device pointers that must
+ * outlive the runner) except q/k/v, which are packed into one [q;k;v] weight
+ * owned by the runner at create. */
+typedef struct rq_llama_config {
+    int32_t n_layers;
+    int32_t hidden;       /* = n_heads * head_dim                            */
+    int32_t n_heads;
+    int32_t n_kv_heads;   /* n_heads % n_kv_heads == 0 (GQA)                  */
+    int32_t head_dim;     /* 64 or 128                                        */
+    int32_t intermediate;
+    int32_t vocab;
+    int32_t max_seq;      /* KV cache capacity in tokens, <= 32768            */
+    float norm_eps;       /* RMSNorm epsilon (1e-5 in the reference)          */
+    float rope_theta;     /* RoPE base (10000 in the reference)               */
+} rq_llama_config;
+
+/* One LlamaBlock's weights.  Norm weights are fp16 [hidden]; Linear weights
+ * are per-row int8 (RQ_Q_ROWWISE_I8) in [out, in] orientation:
+ * q [n_heads*head_dim, hidden], k/v [n_kv_heads*head_dim, hidden],
+ * o [hidden, n_heads*head_dim], gate/up [intermediate, hidden],
+ * down [hidden, intermediate]. */
+typedef struct rq_llama_layer {
+    const void *attn_norm; /* input_layernorm            */
+    rq_qweight q, k, v, o;
+    const void *mlp_norm;  /* post_attention_layernorm   */
+    rq_qweight gate, up, down;
+} rq_llama_layer;
+
+typedef struct rq_llama_weights {
+    const void *embed;             /* fp16 [vocab, hidden]                 */
+    const rq_llama_layer *layers;  /* host array of n_layers               */
+    const void *final_norm;        /* fp16 [hidden]                        */
+    rq_qweight lm_head;            /* int8 per-row [vocab, hidden]         */
+} rq_llama_weights;
+
+typedef struct rq_llama rq_llama;
+
+/* Validates the weights against the config, packs q/k/v, allocates the KV
+ * cache and step state, and captures the step graph on the context stream. */
+int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weights *w, rq_llama **out);
+int rq_llama_destroy(rq_llama *model);
+/* Starts a sequence: runs the n prompt tokens (host array, each < vocab)
+ * through the model one position at a time, filling the KV cache; the last
+ * step's greedy token becomes token n of the sequence.  Asynchronous. */
+int rq_llama_prefill(rq_llama *model, const int32_t *tokens, int32_t n, rq_stream stream);
+/* n_steps greedy decode steps, each feeding the previous token.  The
+ * sequence grows by n_steps; fails with RQ_ERR_SHAPE past max_seq cached
+ * positions.  Asynchronous (graph launches only). */
+int rq_llama_decode(rq_llama *model, int32_t n_steps, rq_stream stream);
+/* Steps run as one graph launch each (default, use_graph = 1) or as direct
+ * kernel launches on the stream (0: for tools that do not trace graphs). */
+int rq_llama_set_graph(rq_llama *model, int use_graph);
+/* Copies up to `capacity` tokens of the sequence (prompt, then generated) to
+ * host memory and stores the sequence length in *length.  Synchronizes. */
+int rq_llama_tokens(rq_llama *model, int32_t *out, int32_t capacity, int32_t *length, rq_stream stream);
+/* Copies the last step's f32 logits [vocab] to host memory.  Synchronizes. */
+int rq_llama_logits(rq_llama *model, float *out, rq_stream stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

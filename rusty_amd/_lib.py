@@ -42,6 +42,44 @@ class rq_qweight(ctypes.Structure):
     ]
 
 
+class rq_llama_config(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", c_int32),
+        ("hidden", c_int32),
+        ("n_heads", c_int32),
+        ("n_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("intermediate", c_int32),
+        ("vocab", c_int32),
+        ("max_seq", c_int32),
+        ("norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+    ]
+
+
+class rq_llama_layer(ctypes.Structure):
+    _fields_ = [
+        ("attn_norm", c_void_p),
+        ("q", rq_qweight),
+        ("k", rq_qweight),
+        ("v", rq_qweight),
+        ("o", rq_qweight),
+        ("mlp_norm", c_void_p),
+        ("gate", rq_qweight),
+        ("up", rq_qweight),
+        ("down", rq_qweight),
+    ]
+
+
+class rq_llama_weights(ctypes.Structure):
+    _fields_ = [
+        ("embed", c_void_p),
+        ("layers", POINTER(rq_llama_layer)),
+        ("final_norm", c_void_p),
+        ("lm_head", rq_qweight),
+    ]
+
+
 _P = c_void_p
 # name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -67,6 +105,13 @@ _SIGNATURES = {
     "rq_qmatmul": [_P, POINTER(rq_qweight), _P, c_int, _P, c_int, c_int64, _P],
     "rq_mlp_swiglu": [_P, POINTER(rq_qweight), POINTER(rq_qweight), POINTER(rq_qweight), _P, c_int, _P, _P, c_int,
                       c_int64, _P],
+    "rq_llama_create": [_P, POINTER(rq_llama_config), POINTER(rq_llama_weights), POINTER(c_void_p)],
+    "rq_llama_destroy": [_P],
+    "rq_llama_prefill": [_P, POINTER(c_int32), c_int32, _P],
+    "rq_llama_decode": [_P, c_int32, _P],
+    "rq_llama_set_graph": [_P, c_int],
+    "rq_llama_tokens": [_P, POINTER(c_int32), c_int32, POINTER(c_int32), _P],
+    "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }
 _RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p}
 

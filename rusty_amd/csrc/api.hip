@@ -9,12 +9,6 @@
 
 #include "common.hpp"
 
-struct rq_ctx {
-    int device;
-    hipStream_t stream;
-    int num_cus;
-};
-
 namespace rq {
 
 static thread_local char g_err[512];
@@ -27,7 +21,7 @@ int fail(int status, const char *fmt, ...) {
     return status;
 }
 
-static int enter(rq_ctx *ctx) {
+int enter(rq_ctx *ctx) {
     g_err[0] = '\0';
     if (!ctx) return fail(RQ_ERR_INVALID_ARGUMENT, "null context");
     int cur = -1;
@@ -36,10 +30,7 @@ static int enter(rq_ctx *ctx) {
     return RQ_OK;
 }
 
-static hipStream_t pick(rq_ctx *ctx, rq_stream s) { return s ? static_cast<hipStream_t>(s) : ctx->stream; }
-
-// a*b without overflow; false if it does not fit in int64.
-static bool mul_ok(int64_t a, int64_t b, int64_t *out) {
+bool mul_ok(int64_t a, int64_t b, int64_t *out) {
     if (a < 0 || b < 0) return false;
     if (a != 0 && b > INT64_MAX / a) return false;
     *out = a * b;
@@ -50,11 +41,19 @@ static bool mul_ok(int64_t a, int64_t b, int64_t *out) {
 
 using namespace rq;
 
-#define RQ_ENTER(ctx)                      \
-    do {                                   \
-        int rq_st_ = ::rq::enter(ctx);     \
-        if (rq_st_ != RQ_OK) return rq_st_; \
-    } while (0)
+int rq::check_qweight(const rq_qweight *w) {
+    if (!w) return fail(RQ_ERR_INVALID_ARGUMENT, "null weight");
+    if (w->format != RQ_Q_ROWWISE_I8 && w->format != RQ_Q_AFFINE_U8)
+        return fail(RQ_ERR_INVALID_ARGUMENT, "unknown weight format %d", w->format);
+    if (w->n_out < 0 || w->k_in < 0) return fail(RQ_ERR_SHAPE, "negative weight shape");
+    int64_t n;
+    if (!mul_ok(w->n_out, w->k_in, &n)) return fail(RQ_ERR_SHAPE, "weight shape overflows");
+    if (w->format == RQ_Q_AFFINE_U8 && w->group <= 0)
+        return fail(RQ_ERR_INVALID_ARGUMENT, "affine weight needs group > 0");
+    if (n > 0 && !w->codes) return fail(RQ_ERR_INVALID_ARGUMENT, "null codes");
+    if (w->n_out > 0 && !w->scales) return fail(RQ_ERR_INVALID_ARGUMENT, "null scales");
+    return RQ_OK;
+}
 
 extern "C" {
 
@@ -210,19 +209,6 @@ int rq_affine_dequantize(rq_ctx *ctx, const uint32_t *weight, size_t n_weight_wo
                                     pick(ctx, stream));
 }
 
-static int check_qweight(const rq_qweight *w) {
-    if (!w) return fail(RQ_ERR_INVALID_ARGUMENT, "null weight");
-    if (w->format != RQ_Q_ROWWISE_I8 && w->format != RQ_Q_AFFINE_U8)
-        return fail(RQ_ERR_INVALID_ARGUMENT, "unknown weight format %d", w->format);
-    if (w->n_out < 0 || w->k_in < 0) return fail(RQ_ERR_SHAPE, "negative weight shape");
-    int64_t n;
-    if (!mul_ok(w->n_out, w->k_in, &n)) return fail(RQ_ERR_SHAPE, "weight shape overflows");
-    if (w->format == RQ_Q_AFFINE_U8 && w->group <= 0)
-        return fail(RQ_ERR_INVALID_ARGUMENT, "affine weight needs group > 0");
-    if (n > 0 && !w->codes) return fail(RQ_ERR_INVALID_ARGUMENT, "null codes");
-    if (w->n_out > 0 && !w->scales) return fail(RQ_ERR_INVALID_ARGUMENT, "null scales");
-    return RQ_OK;
-}
 
 int rq_qweight_dequantize(rq_ctx *ctx, const rq_qweight *w, float *out, rq_stream stream) {
     RQ_ENTER(ctx);
@@ -270,7 +256,7 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 // Fused linear dispatch (arguments already validated): decode kernels for
 // few tokens, the MFMA GEMM for many, the generic kernel for anything the
 // tuned paths do not serve.
-static int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
+int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                             int64_t m, hipStream_t s) {
     if (w.k_in > 0) {
         int st = RQ_ERR_UNSUPPORTED;

@@ -8,6 +8,14 @@
 
 #include "rusty_hip.h"
 
+// A device context: the device ordinal, the context's own stream (default
+// priority) and the device's compute-unit count.
+struct rq_ctx {
+    int device;
+    hipStream_t stream;
+    int num_cus;
+};
+
 namespace rq {
 
 // Records a message for rq_last_error() and returns `status`.
@@ -25,6 +33,20 @@ int fail(int status, const char *fmt, ...);
 // Launch check: kernel launches report configuration errors via hipGetLastError.
 #define RQ_LAUNCH_CHECK() RQ_HIP_TRY(hipGetLastError())
 
+// Clears the calling thread's error message and makes ctx's device current.
+int enter(rq_ctx *ctx);
+inline hipStream_t pick(rq_ctx *ctx, rq_stream s) { return s ? static_cast<hipStream_t>(s) : ctx->stream; }
+// a*b without overflow; false if it does not fit in int64 (or is negative).
+bool mul_ok(int64_t a, int64_t b, int64_t *out);
+// Validates an rq_qweight descriptor (format, shape, null pointers).
+int check_qweight(const rq_qweight *w);
+
+#define RQ_ENTER(ctx)                       \
+    do {                                    \
+        int rq_st_ = ::rq::enter(ctx);      \
+        if (rq_st_ != RQ_OK) return rq_st_; \
+    } while (0)
+
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -39,6 +61,13 @@ int launch_rowwise_dequantize(const int8_t *q, const float *scales, float *out, 
 int launch_matmul_f32(int variant, const float *a, const float *b, float *out, int64_t m, int64_t k,
                       int64_t n, hipStream_t s);
 int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
+// m = 1..4 decode GEMV that adds its result into an f32 y (y += X . deq(W)^T):
+// the residual connection fused into the projection's epilogue.
+int launch_gemv_decode_add(const rq_qweight &w, const void *x, float *y, int m, hipStream_t s);
+// m = 1 decode GEMV whose activation row is RMSNorm(x) . nw, computed in the
+// kernel's prologue from the f32 row x (no separate norm launch); f32 y.
+int launch_gemv_decode_norm(const rq_qweight &w, const float *x, const _Float16 *nw, float eps, float *y,
+                            hipStream_t s);
 int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
 int launch_gemv(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m,
                 int num_cus, hipStream_t s);
@@ -47,10 +76,17 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                            int64_t m, hipStream_t s);
 int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
+// SwiGLU gate/up pass over RMSNorm(x) . nw (m = 1, f32 x), h fp16.
+int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
+                              float eps, void *h, hipStream_t s);
 int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
 int launch_swiglu_generic(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h,
                           int64_t m, hipStream_t s);
 int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_t s);
+
+// Y = X . deq(W)^T over every kernel family, picked by m, dtypes and shape.
+int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
+                     hipStream_t s);
 
 enum MatmulVariant { MM_AB = 0, MM_ABT = 1, MM_ATB = 2 };
 

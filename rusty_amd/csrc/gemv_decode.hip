@@ -31,6 +31,8 @@ namespace {
 
 constexpr int DT = 256;
 constexpr uint32_t kOOB = 0x80000000u;  // any offset past a resource reads zero
+// output modes: f32 store, fp16 store, f32 accumulate (y += result)
+constexpr int kYF32 = 0, kYF16 = 1, kYAdd = 2;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -74,13 +76,21 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // SWI: SwiGLU gate/up pass (rowwise only) -- W/scales are the gate weight,
 // W2/scales2 the up weight of the same shape; the block loads R gate rows and
 // the same R up rows per row group and writes h = silu(g) * u (fp16).
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI>
+// NORM (m = 1): the activation row is RMSNorm(x) computed in the prologue
+// from the f32 row Xf and the fp16 norm weight NW (kernels.wgsl:87-102):
+// xn = fp16((x * inv) * nw), inv = 1 / sqrt(mean(x^2) + eps).  Each block
+// reduces the sum of squares itself (one barrier) after its weight loads are
+// in flight, so the norm costs no launch and hides under the weight stream.
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
                                                     const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
-                                                    const _Float16 *__restrict__ X, void *__restrict__ Yv,
-                                                    int y_f16, int m_act, int N, int K, int group) {
+                                                    const _Float16 *__restrict__ X, const float *__restrict__ Xf,
+                                                    const _Float16 *__restrict__ NW, float eps,
+                                                    void *__restrict__ Yv, int ymode, int m_act, int N, int K,
+                                                    int group) {
     static_assert(!SWI || FMT == 0, "SwiGLU pass is rowwise only");
+    static_assert(!NORM || M == 1, "the fused norm serves one activation row");
     constexpr int RP = DT / TPR;
     constexpr int ROWS = R * RP;
     constexpr int TASKS = ROWS * M;
@@ -93,17 +103,32 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     const int row0 = blockIdx.x * ROWS;
 
     // X slice (issued first so its wait does not cover the weight stream).
-    const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
     uint32_t xh[CPT][M][8];
+    uint4 xf4[NORM ? CPT : 1][4], nw4[NORM ? CPT : 1][2];
+    if constexpr (NORM) {
+        const auto rxf = make_rsrc(Xf, (uint32_t)K * 4u);
+        const auto rnw = make_rsrc(NW, (uint32_t)K * 2u);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = tt + TPR * j;
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+            const uint32_t off = c < C ? (uint32_t)c * 64u : kOOB, offw = c < C ? (uint32_t)c * 32u : kOOB;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const uint32_t off = c < C ? ((uint32_t)m * K + (uint32_t)c * 16) * 2u : kOOB;
-            const uint4 a = bload<0>(rx, off), b = bload<0>(rx, off + 16);
-            xh[j][m][0] = a.x; xh[j][m][1] = a.y; xh[j][m][2] = a.z; xh[j][m][3] = a.w;
-            xh[j][m][4] = b.x; xh[j][m][5] = b.y; xh[j][m][6] = b.z; xh[j][m][7] = b.w;
+            for (int q = 0; q < 4; ++q) xf4[j][q] = bload<0>(rxf, off + 16 * q);
+            nw4[j][0] = bload<0>(rnw, offw);
+            nw4[j][1] = bload<0>(rnw, offw + 16);
+        }
+    } else {
+        const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint32_t off = c < C ? ((uint32_t)m * K + (uint32_t)c * 16) * 2u : kOOB;
+                const uint4 a = bload<0>(rx, off), b = bload<0>(rx, off + 16);
+                xh[j][m][0] = a.x; xh[j][m][1] = a.y; xh[j][m][2] = a.z; xh[j][m][3] = a.w;
+                xh[j][m][4] = b.x; xh[j][m][5] = b.y; xh[j][m][6] = b.z; xh[j][m][7] = b.w;
+            }
         }
     }
     // Weight chunks: R rows x CPT chunks per thread, all in flight.
@@ -119,6 +144,43 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             const uint32_t off = c < C ? (uint32_t)((r % R) * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
             w[r][j] = bload<2>(r < R ? rw : rw2, off);
         }
+    if constexpr (NORM) {
+        // sum of squares over row group 0 (each row group holds all of x)
+        __shared__ float nred[DT / 64];
+        float ss = 0.0f;
+        if (rp == 0) {
+#pragma unroll
+            for (int j = 0; j < CPT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float f[4] = {__builtin_bit_cast(float, xf4[j][q].x), __builtin_bit_cast(float, xf4[j][q].y),
+                                        __builtin_bit_cast(float, xf4[j][q].z), __builtin_bit_cast(float, xf4[j][q].w)};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+                }
+        }
+        ss = wave_total(ss);
+        if (lane == 0) nred[wave] = ss;
+        __syncthreads();
+        ss = (nred[0] + nred[1]) + (nred[2] + nred[3]);
+        const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 xv = xf4[j][q];
+                const float f[4] = {__builtin_bit_cast(float, xv.x), __builtin_bit_cast(float, xv.y),
+                                    __builtin_bit_cast(float, xv.z), __builtin_bit_cast(float, xv.w)};
+                // norm weights of elements 4q..4q+3: halves 4q..4q+3 of the 16 in nw4[j]
+                const uint4 nv = nw4[j][q >> 1];
+                const uint32_t n01 = (q & 1) ? nv.z : nv.x, n23 = (q & 1) ? nv.w : nv.y;
+                const h2_t a = __builtin_bit_cast(h2_t, n01), b = __builtin_bit_cast(h2_t, n23);
+                const h2_t lo = {(_Float16)((f[0] * inv) * (float)a.x), (_Float16)((f[1] * inv) * (float)a.y)};
+                const h2_t hi = {(_Float16)((f[2] * inv) * (float)b.x), (_Float16)((f[3] * inv) * (float)b.y)};
+                xh[j][0][2 * q] = __builtin_bit_cast(uint32_t, lo);
+                xh[j][0][2 * q + 1] = __builtin_bit_cast(uint32_t, hi);
+            }
+    }
     float sg[R][CPT], bg[R][CPT];
     if constexpr (FMT == 1) {
 #pragma unroll
@@ -209,75 +271,100 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             float y = FMT == 0 ? tot * scales[row] : tot;
             if constexpr (SWI) y = silu(y) * (tot2 * scales2[row]);
             const size_t o = (size_t)m * N + row;
-            if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
+            if (ymode == kYF16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
+            else if (ymode == kYAdd) reinterpret_cast<float *>(Yv)[o] += y;
             else reinterpret_cast<float *>(Yv)[o] = y;
         }
     }
 }
 
 using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
-                          const _Float16 *, void *, int, int, int, int, int);
+                          const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int);
 
 // fmt 2 selects the SwiGLU gate/up pass.  Rows per row group: 2 at m = 1,
 // else 4 (SwiGLU: pairs, so the same number of weight bytes per block).
+// norm (m = 1, per-row codes only): the fused RMSNorm prologue.
 template <int M, int CPT, int TPR>
-DecodeFn pick_fmt(int fmt) {
+DecodeFn pick_fmt(int fmt, bool norm) {
     constexpr int R = M == 1 ? 2 : 4;
-    if (fmt == 2) return &k_gemv_decode<M, CPT, TPR, R / 2, 0, true>;
-    return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, R, 0, false> : &k_gemv_decode<M, CPT, TPR, R, 1, false>;
+    if constexpr (M == 1) {
+        if (norm) return fmt == 2 ? &k_gemv_decode<M, CPT, TPR, R / 2, 0, true, true>
+                                  : &k_gemv_decode<M, CPT, TPR, R, 0, false, true>;
+    }
+    if (fmt == 2) return &k_gemv_decode<M, CPT, TPR, R / 2, 0, true, false>;
+    return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, R, 0, false, false> : &k_gemv_decode<M, CPT, TPR, R, 1, false, false>;
 }
 
 template <int M, int CPT>
-DecodeFn pick_tpr(int tpr, int fmt) {
+DecodeFn pick_tpr(int tpr, int fmt, bool norm) {
     switch (tpr) {
-    case 64: return pick_fmt<M, CPT, 64>(fmt);
-    case 128: return pick_fmt<M, CPT, 128>(fmt);
-    default: return pick_fmt<M, CPT, 256>(fmt);
+    case 64: return pick_fmt<M, CPT, 64>(fmt, norm);
+    case 128: return pick_fmt<M, CPT, 128>(fmt, norm);
+    default: return pick_fmt<M, CPT, 256>(fmt, norm);
     }
 }
 
 template <int M>
-DecodeFn pick_cpt(int cpt, int tpr, int fmt) {
+DecodeFn pick_cpt(int cpt, int tpr, int fmt, bool norm) {
     switch (cpt) {
-    case 1: return pick_tpr<M, 1>(tpr, fmt);
-    case 2: return pick_tpr<M, 2>(tpr, fmt);
-    case 3: return pick_tpr<M, 3>(tpr, fmt);
-    default: return pick_tpr<M, 4>(tpr, fmt);
+    case 1: return pick_tpr<M, 1>(tpr, fmt, norm);
+    case 2: return pick_tpr<M, 2>(tpr, fmt, norm);
+    case 3: return pick_tpr<M, 3>(tpr, fmt, norm);
+    default: return pick_tpr<M, 4>(tpr, fmt, norm);
     }
 }
 
 }  // namespace
 
-static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, void *y, rq_dtype yt, int m,
-                         hipStream_t s) {
+// x: fp16 activations, or (nw != null, m = 1) the f32 row to RMS-normalise
+// with the fp16 weight nw and epsilon eps.
+static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, const _Float16 *nw, float eps,
+                         void *y, int ymode, int m, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
         !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && w.group % 16 != 0))
         return RQ_ERR_UNSUPPORTED;
     if (w2 && (w.format != RQ_Q_ROWWISE_I8 || w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16)))
         return RQ_ERR_UNSUPPORTED;
+    if (nw && (m != 1 || w.format != RQ_Q_ROWWISE_I8 || !aligned(nw, 16))) return RQ_ERR_UNSUPPORTED;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
     const int cpt = (int)cdiv(C, tpr);
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
     const int fmt = w2 ? 2 : w.format;
-    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt) : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt)
-                                                                 : pick_cpt<4>(cpt, tpr, fmt);
+    const bool norm = nw != nullptr;
+    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm) : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false)
+                                                                       : pick_cpt<4>(cpt, tpr, fmt, false);
     const int rows = (mt == 1 ? 2 : 4) / (w2 ? 2 : 1) * (DT / tpr);
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
-                       w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, (const _Float16 *)x, y,
-                       yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.group);
+                       w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr,
+                       norm ? nullptr : (const _Float16 *)x, norm ? (const float *)x : nullptr, nw, eps, y, ymode, m,
+                       (int)N, (int)K, w.group);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 
 int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
-    return launch_decode(w, nullptr, x, y, yt, m, s);
+    return launch_decode(w, nullptr, x, nullptr, 0.0f, y, yt == RQ_F16 ? kYF16 : kYF32, m, s);
+}
+
+int launch_gemv_decode_add(const rq_qweight &w, const void *x, float *y, int m, hipStream_t s) {
+    return launch_decode(w, nullptr, x, nullptr, 0.0f, y, kYAdd, m, s);
+}
+
+int launch_gemv_decode_norm(const rq_qweight &w, const float *x, const _Float16 *nw, float eps, float *y,
+                            hipStream_t s) {
+    return launch_decode(w, nullptr, x, nw, eps, y, kYF32, 1, s);
 }
 
 int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s) {
-    return launch_decode(gate, &up, x, h, RQ_F16, m, s);
+    return launch_decode(gate, &up, x, nullptr, 0.0f, h, kYF16, m, s);
+}
+
+int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
+                              float eps, void *h, hipStream_t s) {
+    return launch_decode(gate, &up, x, nw, eps, h, kYF16, 1, s);
 }
 
 }  // namespace rq

@@ -1,0 +1,605 @@
+// Int8-weight Llama decode runner: one greedy decode step of a LlamaModel
+// (rusty-graph/src/lib.rs:420-436) as a HIP graph of 5 launches per block
+// plus 2 at the end, replayed once per token with no host round trip.
+//
+// Per block (LlamaBlock::forward, rusty-graph/src/lib.rs:364-378):
+//   qkv  = rmsnorm(x, attn_norm) . [Wq;Wk;Wv]^T   decode GEMV with the RMSNorm
+//                                                 in its prologue (q, k, v
+//                                                 packed into one weight)
+//   attn = softmax(rope(q) . K^T / sqrt(d)) . V   k_attn_decode (RoPE, KV
+//                                                 append, GQA attention)
+//   x   += attn . Wo^T                            decode GEMV, add epilogue
+//   h    = silu(xn . Wg^T) * (xn . Wu^T),         fused gate/up decode GEMV,
+//          xn = rmsnorm(x, mlp_norm)              norm in its prologue
+//   x   += h . Wd^T                               decode GEMV, add epilogue
+// then logits = rmsnorm(x, final_norm) . Wlm^T (norm fused likewise) and
+// k_argmax_embed picks the greedy token (top_k with k = 1,
+// kernels.wgsl:173-188), appends it to the sequence and gathers its embedding
+// row into x for the next step (Embedding::forward, rusty-graph/src/lib.rs:
+// 121-135, done on the device).
+//
+// All state the step reads (position, token sequence, residual x, KV cache)
+// lives in device memory, so the same instantiated graph serves every
+// position.  The residual stream x is f32; activations entering a GEMV are
+// fp16; the KV cache is fp16 in [layer][kv_head][position][head_dim] order.
+#include <math.h>
+
+#include <new>
+#include <vector>
+
+#include "common.hpp"
+
+struct rq_llama {
+    struct Layer {
+        const _Float16 *attn_norm, *mlp_norm;
+        rq_qweight qkv, o, gate, up, down;
+    };
+    rq_ctx *ctx = nullptr;
+    rq_llama_config cfg{};
+    std::vector<Layer> layers;
+    const _Float16 *embed = nullptr, *final_norm = nullptr;
+    rq_qweight lm_head{};
+    void *owned = nullptr;  // packed qkv weights + step state, one allocation
+    float *x = nullptr, *qkv_out = nullptr, *logits = nullptr;
+    _Float16 *attn = nullptr, *h = nullptr, *kc = nullptr, *vc = nullptr;
+    int *tokens = nullptr, *pos = nullptr, *n_prompt = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool use_graph = true;
+    int host_pos = 0;  // tokens already in the KV cache (the next step's position)
+    int host_len = 0;  // tokens in the sequence, prompt + generated
+};
+
+namespace rq {
+namespace {
+
+constexpr int NT = 256;
+constexpr int kMaxSeq = 32768;  // KV cache capacity limit (32-bit cache offsets)
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+constexpr uint32_t kOOB = 0x80000000u;  // any offset past a buffer resource reads zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void widen8(const uint4 u, float *f) {
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2_t p = __builtin_bit_cast(h2_t, wd[i]);
+        f[2 * i] = (float)p.x;
+        f[2 * i + 1] = (float)p.y;
+    }
+}
+
+// Threads per attention block: 16 waves for head_dim 64, 8 for 128 (register
+// budget of the in-flight K and V rows).
+template <int HD>
+constexpr int attn_threads() { return HD == 64 ? 1024 : 512; }
+
+// Decode attention of query head blockIdx.x at position pos = *pos_p.
+// RoPE (kernels.wgsl:60-79, rotate-half: dims d and d + HD/2 by the angle
+// pos * theta^(-2d/HD)) is applied to q and to the new key; the block of the
+// first query head of each KV group appends the new key and value (rounded to
+// fp16) to the cache at `pos` (rusty-graph/src/lib.rs:235-246).  Every block
+// uses the fp16-rounded new key/value for position pos and reads the cache
+// only below pos (the buffer resource ends there; rows past it read as zero),
+// so no block reads what another block of this launch writes.
+// Scores q.k / sqrt(HD) over positions 0..pos (causal), softmax in f32,
+// output fp16 [n_heads * HD].  GQA: query head h reads KV head
+// h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
+//
+// Memory-latency bound (tens of KB per head), so the loads are shaped for
+// one round trip per pass: a pass covers AT positions, each wave 64
+// consecutive rows (8 or 16 KB contiguous for K and for V); lane l loads
+// 16-byte chunk l % CH of row (i * 64 + l) / CH for i < CH, all K and V loads
+// issued before any is used.  Row scores are finished by xor-shuffles over
+// the CH lanes of a row; P.V partials per lane are summed over the lanes of
+// the same chunk, then over waves in LDS.  Passes beyond the first (pos >= AT)
+// combine by the online-softmax rescale.
+template <int HD>
+__global__ __launch_bounds__(attn_threads<HD>()) void k_attn_decode(
+    const float *__restrict__ qkv, _Float16 *__restrict__ kc, _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
+    _Float16 *__restrict__ out, int n_heads, int n_kv, int max_seq, float theta) {
+    constexpr int AT = attn_threads<HD>(), NW = AT / 64;
+    constexpr int CH = HD / 8;    // 16-byte chunks per row
+    constexpr int RPI = 64 / CH;  // rows per wave-wide load
+    constexpr int HALF = HD / 2;
+    __shared__ float qs[HD], kn[HD], vn[HD], redm[NW], reds[NW];
+    __shared__ float accs[NW][HD];
+    const int hd = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int pos = *pos_p;
+    const int grp = n_heads / n_kv, g = hd / grp;
+    const float *q = qkv + (size_t)hd * HD;
+    const float *k = qkv + (size_t)n_heads * HD + (size_t)g * HD;
+    const float *v = qkv + (size_t)(n_heads + n_kv) * HD + (size_t)g * HD;
+    if (t < HALF) {
+        const float inv_freq = powf(theta, -2.0f * (float)t / (float)HD);
+        float sn, cs;
+        sincosf((float)pos * inv_freq, &sn, &cs);
+        const float q1 = q[t], q2 = q[t + HALF], k1 = k[t], k2 = k[t + HALF];
+        qs[t] = q1 * cs - q2 * sn;
+        qs[t + HALF] = q1 * sn + q2 * cs;
+        kn[t] = (float)(_Float16)(k1 * cs - k2 * sn);
+        kn[t + HALF] = (float)(_Float16)(k1 * sn + k2 * cs);
+    }
+    if (t < HD) vn[t] = (float)(_Float16)v[t];
+    __syncthreads();
+    _Float16 *kcg = kc + (size_t)g * max_seq * HD;
+    _Float16 *vcg = vc + (size_t)g * max_seq * HD;
+    if (hd % grp == 0 && t < HD) {
+        kcg[(size_t)pos * HD + t] = (_Float16)kn[t];
+        vcg[(size_t)pos * HD + t] = (_Float16)vn[t];
+    }
+    const auto rk = make_rsrc(kcg, (uint32_t)pos * HD * 2u);
+    const auto rv = make_rsrc(vcg, (uint32_t)pos * HD * 2u);
+    const int ch = lane % CH, rl = lane / CH;
+    float qv[8], knv[8], vnv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        qv[e] = qs[ch * 8 + e];
+        knv[e] = kn[ch * 8 + e];
+        vnv[e] = vn[ch * 8 + e];
+    }
+    // score of the new key (position pos), reduced over the CH lanes of a row
+    float s_new = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_new = fmaf(qv[e], knv[e], s_new);
+#pragma unroll
+    for (int o = 1; o < CH; o <<= 1) s_new += __shfl_xor(s_new, o, 64);
+
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int T = pos + 1;
+    float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int c0 = 0; c0 < T; c0 += AT) {
+        const int base = c0 + 64 * w;
+        uint4 kr[CH], vr[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int row = base + i * RPI + rl;
+            const uint32_t off = row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
+            kr[i] = bload(rk, off);
+            vr[i] = bload(rv, off);
+        }
+        float sv[CH];
+        float lm = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            float f[8], s = 0.0f;
+            widen8(kr[i], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = fmaf(qv[e], f[e], s);
+#pragma unroll
+            for (int o = 1; o < CH; o <<= 1) s += __shfl_xor(s, o, 64);
+            const int row = base + i * RPI + rl;
+            s = row == pos ? s_new : s;
+            sv[i] = row < T ? s * scale : -__builtin_inff();
+            lm = fmaxf(lm, sv[i]);
+        }
+        lm = wave_max(lm);
+        if (lane == 0) redm[w] = lm;
+        __syncthreads();
+        float cm = redm[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) cm = fmaxf(cm, redm[i]);
+        const float m_new = fmaxf(m_run, cm);  // finite: row 0 is in the first pass
+        const float alpha = expf(m_run - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const float p = expf(sv[i] - m_new);
+            const int row = base + i * RPI + rl;
+            float f[8];
+            widen8(vr[i], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, row == pos ? vnv[e] : f[e], acc[e]);
+            ls += ch == 0 ? p : 0.0f;  // one lane per row counts it
+        }
+        ls = wave_sum(ls);
+        if (lane == 0) reds[w] = ls;
+        __syncthreads();
+        float cl = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) cl += reds[i];
+        l_run = l_run * alpha + cl;
+        m_run = m_new;
+        __syncthreads();  // redm / reds are rewritten by the next pass
+    }
+    // sum P.V partials over the lanes holding the same chunk, then over waves
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int o = CH; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o, 64);
+    if (rl == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) accs[w][ch * 8 + e] = acc[e];
+    }
+    __syncthreads();
+    if (t < HD) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) sum += accs[i][t];
+        out[(size_t)hd * HD + t] = (_Float16)(sum / l_run);
+    }
+}
+
+constexpr int AT = 1024;
+
+// Greedy pick + embedding gather, one block.  The step processed the token at
+// position pos = *pos_p.  The next token is the prompt's token pos + 1 while
+// the prompt lasts (teacher forcing during prefill), else the argmax of the
+// logits: the first index of the largest value greater than -1e9, index 0 if
+// none (the reference's top_k scan, kernels.wgsl:177-186).  It is stored at
+// tokens[pos + 1], its fp16 embedding row is widened into x, and *pos_p
+// advances by one.
+__global__ __launch_bounds__(AT) void k_argmax_embed(const float *__restrict__ logits, int V,
+                                                     const _Float16 *__restrict__ embed, int H,
+                                                     int *__restrict__ tokens, int *__restrict__ pos_p,
+                                                     const int *__restrict__ n_prompt_p, float *__restrict__ x) {
+    __shared__ float bv[AT / 64];
+    __shared__ int bi[AT / 64];
+    __shared__ int next_s;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float best = -1e9f;
+    int idx = 0;
+    // each thread scans its indices in ascending order (strict >: the first
+    // of equal maxima), 8 float4 loads in flight per round
+    const auto rl = make_rsrc(logits, (uint32_t)V * 4u);
+    const int n4 = (V + 3) / 4;
+    for (int b = 0; b < n4; b += AT * 8) {
+        uint4 v4[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i4 = b + u * AT + t;
+            v4[u] = bload(rl, i4 < n4 ? (uint32_t)i4 * 16u : kOOB);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t wd[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = (b + u * AT + t) * 4 + e;
+                const float v = __builtin_bit_cast(float, wd[e]);
+                if (i < V && v > best) {
+                    best = v;
+                    idx = i;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    const int pos = *pos_p;
+    if (t == 0) {
+        for (int w = 1; w < AT / 64; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        const int next = pos + 1 < *n_prompt_p ? tokens[pos + 1] : idx;
+        tokens[pos + 1] = next;
+        next_s = next;
+    }
+    __syncthreads();
+    const _Float16 *row = embed + (size_t)next_s * H;
+    for (int i = t; i < H; i += AT) x[i] = (float)row[i];
+    if (t == 0) *pos_p = pos + 1;
+}
+
+// Start of a sequence: x = embed[tokens[0]], pos = 0, prompt length n.
+__global__ __launch_bounds__(NT) void k_embed_start(const int *__restrict__ tokens, const _Float16 *__restrict__ embed,
+                                                    int H, float *__restrict__ x, int *__restrict__ pos_p,
+                                                    int *__restrict__ n_prompt_p, int n_prompt) {
+    const _Float16 *row = embed + (size_t)tokens[0] * H;
+    for (int i = threadIdx.x; i < H; i += NT) x[i] = (float)row[i];
+    if (threadIdx.x == 0) {
+        *pos_p = 0;
+        *n_prompt_p = n_prompt;
+    }
+}
+
+int enqueue_step(rq_llama *md, hipStream_t s) {
+    const rq_llama_config &c = md->cfg;
+    const int H = c.hidden;
+    const size_t kv_layer = (size_t)c.n_kv_heads * c.max_seq * c.head_dim;
+    int st;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const rq_llama::Layer &L = md->layers[l];
+        if ((st = launch_gemv_decode_norm(L.qkv, md->x, L.attn_norm, c.norm_eps, md->qkv_out, s)) != RQ_OK)
+            return st;
+        if (c.head_dim == 64)
+            hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads), dim3(attn_threads<64>()), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->attn, c.n_heads,
+                               c.n_kv_heads, c.max_seq, c.rope_theta);
+        else
+            hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads), dim3(attn_threads<128>()), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->attn, c.n_heads,
+                               c.n_kv_heads, c.max_seq, c.rope_theta);
+        RQ_LAUNCH_CHECK();
+        if ((st = launch_gemv_decode_add(L.o, md->attn, md->x, 1, s)) != RQ_OK) return st;
+        if ((st = launch_swiglu_decode_norm(L.gate, L.up, md->x, L.mlp_norm, c.norm_eps, md->h, s)) != RQ_OK)
+            return st;
+        if ((st = launch_gemv_decode_add(L.down, md->h, md->x, 1, s)) != RQ_OK) return st;
+    }
+    if ((st = launch_gemv_decode_norm(md->lm_head, md->x, md->final_norm, c.norm_eps, md->logits, s)) != RQ_OK)
+        return st;
+    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(AT), 0, s, md->logits, c.vocab, md->embed, H, md->tokens, md->pos,
+                       md->n_prompt, md->x);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+// The decode kernels this runner launches take per-row int8 weights with
+// K % 16 == 0 and K <= 16384, 16-byte aligned codes.
+int check_linear(const rq_qweight &w, int64_t n, int64_t k, const char *name, int layer) {
+    int st = check_qweight(&w);
+    if (st != RQ_OK) return st;
+    if (w.n_out != n || w.k_in != k)
+        return fail(RQ_ERR_SHAPE, "layer %d %s: weight is [%lld,%lld], expected [%lld,%lld]", layer, name,
+                    (long long)w.n_out, (long long)w.k_in, (long long)n, (long long)k);
+    if (w.format != RQ_Q_ROWWISE_I8)
+        return fail(RQ_ERR_UNSUPPORTED, "layer %d %s: the decode runner takes per-row int8 weights", layer, name);
+    if (k % 16 != 0 || k > 16384 || !aligned(w.codes, 16))
+        return fail(RQ_ERR_UNSUPPORTED, "layer %d %s: needs k %% 16 == 0, k <= 16384 and 16-byte aligned codes",
+                    layer, name);
+    return RQ_OK;
+}
+
+int run_steps(rq_llama *md, int n, hipStream_t s) {
+    for (int i = 0; i < n; ++i) {
+        if (md->use_graph) {
+            RQ_HIP_TRY(hipGraphLaunch(md->exec, s));
+        } else {
+            const int st = enqueue_step(md, s);
+            if (st != RQ_OK) return st;
+        }
+    }
+    return RQ_OK;
+}
+
+void release(rq_llama *md) {
+    if (md->exec) (void)hipGraphExecDestroy(md->exec);
+    if (md->graph) (void)hipGraphDestroy(md->graph);
+    if (md->owned) (void)hipFree(md->owned);
+    delete md;
+}
+
+template <typename T>
+T *carve(char *&p, size_t count) {
+    T *r = reinterpret_cast<T *>(p);
+    p += (count * sizeof(T) + 255) & ~size_t(255);
+    return r;
+}
+
+}  // namespace
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" {
+
+int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weights *w, rq_llama **out) {
+    RQ_ENTER(ctx);
+    if (!cfg || !w || !out) return fail(RQ_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const rq_llama_config c = *cfg;
+    if (c.n_layers < 1 || c.hidden < 1 || c.n_heads < 1 || c.n_kv_heads < 1 || c.intermediate < 1 || c.vocab < 1 ||
+        c.max_seq < 1 || !(c.norm_eps >= 0.0f) || !(c.rope_theta > 0.0f))
+        return fail(RQ_ERR_SHAPE, "config fields must be positive");
+    if (c.head_dim != 64 && c.head_dim != 128) return fail(RQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+    if (c.n_heads % c.n_kv_heads != 0) return fail(RQ_ERR_SHAPE, "n_heads must be a multiple of n_kv_heads");
+    if (c.max_seq > kMaxSeq) return fail(RQ_ERR_UNSUPPORTED, "max_seq is limited to %d", kMaxSeq);
+    if (!w->embed || !w->layers || !w->final_norm) return fail(RQ_ERR_INVALID_ARGUMENT, "null weight pointer");
+    if (!aligned(w->final_norm, 16)) return fail(RQ_ERR_UNSUPPORTED, "final norm weight must be 16-byte aligned");
+    const int64_t H = c.hidden, QW = (int64_t)c.n_heads * c.head_dim, KW = (int64_t)c.n_kv_heads * c.head_dim;
+    const int64_t QKV = QW + 2 * KW, I = c.intermediate;
+    int st;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const rq_llama_layer &L = w->layers[l];
+        if (!L.attn_norm || !L.mlp_norm) return fail(RQ_ERR_INVALID_ARGUMENT, "layer %d: null norm weight", l);
+        if (!aligned(L.attn_norm, 16) || !aligned(L.mlp_norm, 16))
+            return fail(RQ_ERR_UNSUPPORTED, "layer %d: norm weights must be 16-byte aligned", l);
+        if ((st = check_linear(L.q, QW, H, "q_proj", l)) || (st = check_linear(L.k, KW, H, "k_proj", l)) ||
+            (st = check_linear(L.v, KW, H, "v_proj", l)) || (st = check_linear(L.o, H, QW, "o_proj", l)) ||
+            (st = check_linear(L.gate, I, H, "gate_proj", l)) || (st = check_linear(L.up, I, H, "up_proj", l)) ||
+            (st = check_linear(L.down, H, I, "down_proj", l)))
+            return st;
+    }
+    if ((st = check_linear(w->lm_head, c.vocab, H, "lm_head", -1))) return st;
+
+    rq_llama *md = new (std::nothrow) rq_llama;
+    if (!md) return fail(RQ_ERR_ALLOC, "runner allocation failed");
+    md->ctx = ctx;
+    md->cfg = c;
+    md->embed = static_cast<const _Float16 *>(w->embed);
+    md->final_norm = static_cast<const _Float16 *>(w->final_norm);
+    md->lm_head = w->lm_head;
+
+    // one allocation: per layer packed [q;k;v] codes and scales, then state
+    const size_t L = (size_t)c.n_layers, kv = L * (size_t)c.n_kv_heads * c.max_seq * c.head_dim;
+    auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
+    size_t bytes = L * (pad((size_t)QKV * H) + pad((size_t)QKV * 4));
+    bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(QW * 2) + pad(2 * I * 2) +
+             2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4);
+    hipError_t e = hipMalloc(&md->owned, bytes);
+    if (e != hipSuccess) {
+        md->owned = nullptr;
+        release(md);
+        return fail(RQ_ERR_ALLOC, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    char *p = static_cast<char *>(md->owned);
+    hipStream_t s = ctx->stream;
+    md->layers.resize(L);
+    for (size_t l = 0; l < L; ++l) {
+        const rq_llama_layer &src = w->layers[l];
+        rq_llama::Layer &dst = md->layers[l];
+        uint8_t *codes = carve<uint8_t>(p, (size_t)QKV * H);
+        float *scales = carve<float>(p, (size_t)QKV);
+        const rq_qweight *parts[3] = {&src.q, &src.k, &src.v};
+        size_t row = 0;
+        for (const rq_qweight *pw : parts) {
+            e = hipMemcpyAsync(codes + row * H, pw->codes, (size_t)pw->n_out * H, hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(scales + row, pw->scales, (size_t)pw->n_out * 4, hipMemcpyDeviceToDevice, s);
+            if (e != hipSuccess) {
+                release(md);
+                return fail(RQ_ERR_HIP, "packing q/k/v: %s", hipGetErrorString(e));
+            }
+            row += (size_t)pw->n_out;
+        }
+        dst.qkv = rq_qweight{codes, scales, nullptr, QKV, H, RQ_Q_ROWWISE_I8, 0};
+        dst.o = src.o;
+        dst.gate = src.gate;
+        dst.up = src.up;
+        dst.down = src.down;
+        dst.attn_norm = static_cast<const _Float16 *>(src.attn_norm);
+        dst.mlp_norm = static_cast<const _Float16 *>(src.mlp_norm);
+    }
+    md->x = carve<float>(p, H);
+    md->qkv_out = carve<float>(p, QKV);
+    md->logits = carve<float>(p, c.vocab);
+    md->attn = carve<_Float16>(p, QW);
+    md->h = carve<_Float16>(p, 2 * I);
+    md->kc = carve<_Float16>(p, kv);
+    md->vc = carve<_Float16>(p, kv);
+    md->tokens = carve<int>(p, (size_t)c.max_seq + 1);
+    md->pos = carve<int>(p, 1);
+    md->n_prompt = carve<int>(p, 1);
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        release(md);
+        return fail(RQ_ERR_HIP, "packing q/k/v: %s", hipGetErrorString(e));
+    }
+
+    // capture one step; the graph holds kernel launches only
+    e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        release(md);
+        return fail(RQ_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    }
+    st = enqueue_step(md, s);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(s, &g);
+    md->graph = g;
+    if (st != RQ_OK || e != hipSuccess) {
+        release(md);
+        return st != RQ_OK ? st : fail(RQ_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    }
+    e = hipGraphInstantiate(&md->exec, md->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        md->exec = nullptr;
+        release(md);
+        return fail(RQ_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    *out = md;
+    return RQ_OK;
+}
+
+int rq_llama_destroy(rq_llama *md) {
+    if (!md) return RQ_OK;
+    RQ_ENTER(md->ctx);
+    hipError_t e = hipStreamSynchronize(md->ctx->stream);
+    release(md);
+    if (e != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    return RQ_OK;
+}
+
+int rq_llama_prefill(rq_llama *md, const int32_t *tokens, int32_t n, rq_stream stream) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    if (!tokens) return fail(RQ_ERR_INVALID_ARGUMENT, "null tokens");
+    if (n < 1 || n > md->cfg.max_seq) return fail(RQ_ERR_SHAPE, "prompt length %d outside 1..%d", n, md->cfg.max_seq);
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= md->cfg.vocab)
+            return fail(RQ_ERR_INVALID_ARGUMENT, "token %d at %d outside the vocabulary", tokens[i], i);
+    hipStream_t s = pick(md->ctx, stream);
+    RQ_HIP_TRY(hipMemcpyAsync(md->tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    RQ_HIP_TRY(hipStreamSynchronize(s));  // the host array may be released on return
+    hipLaunchKernelGGL(k_embed_start, dim3(1), dim3(NT), 0, s, md->tokens, md->embed, md->cfg.hidden, md->x, md->pos,
+                       md->n_prompt, n);
+    RQ_LAUNCH_CHECK();
+    int st;
+    if ((st = run_steps(md, n, s)) != RQ_OK) return st;
+    md->host_pos = n;
+    md->host_len = n + 1;
+    return RQ_OK;
+}
+
+int rq_llama_decode(rq_llama *md, int32_t n_steps, rq_stream stream) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    if (md->host_len == 0) return fail(RQ_ERR_INVALID_ARGUMENT, "no sequence: call rq_llama_prefill first");
+    if (n_steps < 0 || n_steps > md->cfg.max_seq - md->host_pos)
+        return fail(RQ_ERR_SHAPE, "%d steps from position %d exceed max_seq %d", n_steps, md->host_pos,
+                    md->cfg.max_seq);
+    hipStream_t s = pick(md->ctx, stream);
+    int st;
+    if ((st = run_steps(md, n_steps, s)) != RQ_OK) return st;
+    md->host_pos += n_steps;
+    md->host_len += n_steps;
+    return RQ_OK;
+}
+
+int rq_llama_set_graph(rq_llama *md, int use_graph) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    md->use_graph = use_graph != 0;
+    return RQ_OK;
+}
+
+int rq_llama_tokens(rq_llama *md, int32_t *out, int32_t capacity, int32_t *length, rq_stream stream) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    if (!length || (capacity > 0 && !out)) return fail(RQ_ERR_INVALID_ARGUMENT, "null output");
+    *length = md->host_len;
+    const int n = capacity < md->host_len ? capacity : md->host_len;
+    if (n <= 0) return RQ_OK;
+    hipStream_t s = pick(md->ctx, stream);
+    RQ_HIP_TRY(hipMemcpyAsync(out, md->tokens, (size_t)n * 4, hipMemcpyDeviceToHost, s));
+    RQ_HIP_TRY(hipStreamSynchronize(s));
+    return RQ_OK;
+}
+
+int rq_llama_logits(rq_llama *md, float *out, rq_stream stream) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    if (!out) return fail(RQ_ERR_INVALID_ARGUMENT, "null output");
+    hipStream_t s = pick(md->ctx, stream);
+    RQ_HIP_TRY(hipMemcpyAsync(out, md->logits, (size_t)md->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
+    RQ_HIP_TRY(hipStreamSynchronize(s));
+    return RQ_OK;
+}
+
+}  // extern "C"

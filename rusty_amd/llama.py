@@ -1,0 +1,168 @@
+"""Greedy int8-weight Llama decode on the device (``rq_llama_*`` of the C ABI).
+
+Host mirror of the reference's ``LlamaModel`` (rusty-graph/src/lib.rs:410-436):
+token embedding (fp16 table), ``n_layers`` LlamaBlocks (RMSNorm -> GQA
+attention with RoPE and a KV cache -> residual add -> RMSNorm -> SwiGLU MLP ->
+residual add, lib.rs:364-378), final RMSNorm and the lm_head projection, with
+greedy (top-1) sampling.  Every Linear is a per-row int8 weight read by the
+fused dequant-GEMV; the whole step runs as one HIP graph on the device
+(librusty_hip.so), with no host round trip between tokens.
+
+The reference has no decode loop (its LlamaModel::forward takes the ids and a
+KV cache but nothing drives generation); the loop defined here is: prefill the
+prompt one position at a time (teacher forcing), then each decode step feeds
+the previous greedy token.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from ._lib import call, rq_llama_config, rq_llama_layer, rq_llama_weights
+from .engine import DType, QuantizedTensor, UnifiedTensor, WgpuContext, _stream
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    n_layers: int = 22
+    hidden: int = 2048
+    n_heads: int = 32
+    n_kv_heads: int = 4
+    head_dim: int = 64
+    intermediate: int = 5632
+    vocab: int = 32000
+    max_seq: int = 640
+    norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    def c_struct(self) -> rq_llama_config:
+        return rq_llama_config(self.n_layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim,
+                               self.intermediate, self.vocab, self.max_seq, self.norm_eps, self.rope_theta)
+
+    def linear_shapes(self) -> dict[str, tuple[int, int]]:
+        """[out, in] of each Linear of one block."""
+        qw, kw = self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim
+        return {"q": (qw, self.hidden), "k": (kw, self.hidden), "v": (kw, self.hidden), "o": (self.hidden, qw),
+                "gate": (self.intermediate, self.hidden), "up": (self.intermediate, self.hidden),
+                "down": (self.hidden, self.intermediate)}
+
+    def weight_bytes(self) -> int:
+        """Int8 code bytes + f32 scale bytes read by one decode step."""
+        per_layer = sum(n * k + 4 * n for n, k in self.linear_shapes().values())
+        return self.n_layers * per_layer + self.vocab * self.hidden + 4 * self.vocab
+
+
+# the 1.1B shape (22 layers, hidden 2048, 32/4 heads of 64,
+# SwiGLU 5632, vocab 32000), 512 prompt + 128 generated tokens
+LLAMA_1B = LlamaConfig()
+
+
+@dataclass
+class LlamaHostWeights:
+    """Host copies: fp16 embed [V,H] and norms [H]; per-row int8 Linears as
+    (codes int8 [out,in], scales f32 [out])."""
+    embed: np.ndarray
+    layers: list[dict] = field(default_factory=list)
+    final_norm: np.ndarray | None = None
+    lm_head: tuple[np.ndarray, np.ndarray] | None = None
+
+
+def synth_weights(cfg: LlamaConfig, seed: int = 0) -> LlamaHostWeights:
+    """Random-init weights of the architecture (no checkpoint is available).
+
+    Linear codes uniform in [-127, 127] with per-row scales ~ U(1.36e-4, 4.09e-4):
+    the dequantized weights have std ~0.02, the usual Llama init, so
+    activations stay O(1) through the layers.  Norm weights 1 + U(-0.1, 0.1),
+    embeddings N(0, 1); all fp16.
+    """
+    g = np.random.default_rng(seed)
+
+    def linear(n, k):
+        q = g.integers(-127, 128, size=(n, k), dtype=np.int8)
+        s = g.uniform(0.02 / 73.3 * 0.5, 0.02 / 73.3 * 1.5, size=n).astype(np.float32)
+        return q, s
+
+    def norm():
+        return (1.0 + g.uniform(-0.1, 0.1, size=cfg.hidden)).astype(np.float16)
+
+    w = LlamaHostWeights(embed=g.standard_normal((cfg.vocab, cfg.hidden), dtype=np.float32).astype(np.float16))
+    for _ in range(cfg.n_layers):
+        layer = {"attn_norm": norm(), "mlp_norm": norm()}
+        for name, (n, k) in cfg.linear_shapes().items():
+            layer[name] = linear(n, k)
+        w.layers.append(layer)
+    w.final_norm = norm()
+    w.lm_head = linear(cfg.vocab, cfg.hidden)
+    return w
+
+
+class LlamaRunner:
+    """Device-resident model + KV cache + captured step graph."""
+
+    def __init__(self, ctx: WgpuContext, cfg: LlamaConfig, weights: LlamaHostWeights):
+        self.ctx, self.cfg = ctx, cfg
+        self._keep = []  # device tensors the runner borrows
+
+        def dev_f16(a):
+            t = UnifiedTensor.new(ctx, np.ascontiguousarray(a, dtype=np.float16), dtype=DType.FP16)
+            self._keep.append(t)
+            return t.ptr
+
+        def dev_q(pair):
+            qt = QuantizedTensor.rowwise(ctx, *pair)
+            self._keep.append(qt)
+            return qt.descriptor()
+
+        layers = (rq_llama_layer * cfg.n_layers)()
+        for i, lw in enumerate(weights.layers):
+            L = layers[i]
+            L.attn_norm = dev_f16(lw["attn_norm"])
+            L.mlp_norm = dev_f16(lw["mlp_norm"])
+            for name in ("q", "k", "v", "o", "gate", "up", "down"):
+                setattr(L, name, dev_q(lw[name]))
+        self._layers = layers
+        cw = rq_llama_weights(dev_f16(weights.embed), layers, dev_f16(weights.final_norm), dev_q(weights.lm_head))
+        self._cfg = cfg.c_struct()
+        handle = ctypes.c_void_p()
+        call("rq_llama_create", ctx.handle, ctypes.byref(self._cfg), ctypes.byref(cw), ctypes.byref(handle))
+        self.handle = handle
+
+    def prefill(self, tokens, stream=None) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        call("rq_llama_prefill", self.handle, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(t.size),
+             _stream(stream))
+
+    def decode(self, n_steps: int, stream=None) -> None:
+        call("rq_llama_decode", self.handle, int(n_steps), _stream(stream))
+
+    def set_graph(self, use_graph: bool) -> None:
+        """Graph launch per step (default) or direct kernel launches."""
+        call("rq_llama_set_graph", self.handle, int(bool(use_graph)))
+
+    def tokens(self, stream=None) -> np.ndarray:
+        n = ctypes.c_int32()
+        call("rq_llama_tokens", self.handle, None, 0, ctypes.byref(n), _stream(stream))
+        out = np.zeros(n.value, dtype=np.int32)
+        call("rq_llama_tokens", self.handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), n.value,
+             ctypes.byref(n), _stream(stream))
+        return out
+
+    def logits(self, stream=None) -> np.ndarray:
+        out = np.zeros(self.cfg.vocab, dtype=np.float32)
+        call("rq_llama_logits", self.handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), _stream(stream))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) and self.handle.value:
+            _lib.lib().rq_llama_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+        self._keep.clear()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,136 @@
+"""GPU parity of the int8 Llama decode runner (rq_llama_*) against the oracle.
+
+The device runs the sequence one position at a time through its KV cache
+(one graph launch per token); the oracle (oracle/llama.py) runs the whole
+sequence at once in float64 with causal attention, teacher-forced on the
+device's tokens.  Checks per step:
+  * logits: max|d| <= TOL * max|logits_ref| for that step;
+  * greedy: the device's token has a reference logit within
+    2 * TOL * max|logits_ref| of the reference maximum (a near tie may pick
+    either index; anything further off is a wrong token).
+TOL = 1e-2 for the small configs, 2e-2 for the 22-layer 1.1B shape: the
+device rounds GEMV inputs, the attention output and the KV cache to fp16
+(relative 2^-11 each), and the difference grows with depth.
+"""
+import numpy as np
+import pytest
+
+from oracle import llama as ol
+from rusty_amd import RqError
+from rusty_amd.llama import LLAMA_1B, LlamaConfig, LlamaRunner, synth_weights
+
+pytestmark = pytest.mark.gpu
+
+TINY = LlamaConfig(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=512, vocab=1000,
+                   max_seq=96)
+
+
+def check_steps(cfg, w, toks, dev_logits, n_prompt, tol, tag):
+    ref = ol.forward(cfg, w, toks[: n_prompt + len(dev_logits) - 1], first=n_prompt - 1)
+    assert ref.shape == dev_logits.shape
+    worst = 0.0
+    for i in range(ref.shape[0]):
+        scale = np.abs(ref[i]).max()
+        d = np.abs(dev_logits[i].astype(np.float64) - ref[i]).max() / scale
+        worst = max(worst, d)
+        tok = toks[n_prompt + i]
+        assert ref[i][tok] >= ref[i].max() - 2 * tol * scale, f"{tag} step {i}: token {tok} is not a greedy pick"
+        assert d <= tol, f"{tag} step {i}: logits rel diff {d:.3e}"
+    print(f"[{tag}] steps={ref.shape[0]} worst logits rel diff {worst:.3e}", flush=True)
+
+
+def run_collect(runner, prompt, steps):
+    runner.prefill(prompt)
+    logits = [runner.logits()]
+    for _ in range(steps):
+        runner.decode(1)
+        logits.append(runner.logits())
+    return runner.tokens(), np.stack(logits)
+
+
+@pytest.mark.parametrize("cfg", [
+    TINY,
+    LlamaConfig(n_layers=2, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, intermediate=384, vocab=777,
+                max_seq=64),
+    LlamaConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=4, head_dim=64, intermediate=256, vocab=300,
+                max_seq=300),
+], ids=["gqa2_hd64", "mqa_hd128", "mha_long"])
+def test_small_models_match_oracle(ctx, cfg):
+    w = synth_weights(cfg, seed=cfg.hidden + cfg.vocab)
+    g = np.random.default_rng(11)
+    n_prompt = min(40, cfg.max_seq // 2) if cfg.max_seq < 200 else 280
+    prompt = g.integers(0, cfg.vocab, n_prompt)
+    steps = cfg.max_seq - n_prompt  # run to full capacity
+    r = LlamaRunner(ctx, cfg, w)
+    toks, logits = run_collect(r, prompt, steps)
+    assert toks.shape == (n_prompt + steps + 1,)
+    np.testing.assert_array_equal(toks[:n_prompt], prompt)
+    check_steps(cfg, w, toks, logits, n_prompt, 1e-2, f"{cfg.n_heads}/{cfg.n_kv_heads}x{cfg.head_dim}")
+    # the cache is full: one more step must be refused
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        r.decode(1)
+    r.close()
+
+
+def test_restart_and_single_token_prompt(ctx):
+    w = synth_weights(TINY, seed=21)
+    r = LlamaRunner(ctx, TINY, w)
+    g = np.random.default_rng(22)
+    p1, p2 = g.integers(0, TINY.vocab, 17), g.integers(0, TINY.vocab, 1)
+    r.prefill(p1)
+    r.decode(9)
+    a = r.tokens()
+    r.prefill(p2)  # a new sequence reuses the cache from position 0
+    r.decode(5)
+    b = r.tokens()
+    r.prefill(p1)
+    r.decode(9)
+    np.testing.assert_array_equal(r.tokens(), a)
+    assert b.shape == (7,) and b[0] == p2[0]
+    ref = ol.forward(TINY, w, b[:6])
+    for i in range(6):
+        assert ref[i][b[i + 1]] >= ref[i].max() - 2e-2 * np.abs(ref[i]).max()
+    r.close()
+
+
+def test_invalid_arguments(ctx):
+    w = synth_weights(TINY, seed=23)
+    r = LlamaRunner(ctx, TINY, w)
+    with pytest.raises(RqError, match="RQ_ERR_INVALID_ARGUMENT"):
+        r.prefill([1, 2, TINY.vocab])
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        r.prefill(np.zeros(TINY.max_seq + 1, dtype=np.int32))
+    with pytest.raises(RqError, match="RQ_ERR_INVALID_ARGUMENT"):
+        r.decode(1)  # no sequence yet
+    r.close()
+    bad = synth_weights(TINY, seed=24)
+    bad.layers[1]["down"] = bad.layers[1]["up"]  # [I, H] where [H, I] is expected
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        LlamaRunner(ctx, TINY, bad)
+
+
+def test_llama_1b_128_greedy_steps(ctx):
+    """1.1B shape, 512-token prompt, 128 greedy decode steps; every
+    generated token and the last step's logits checked against the oracle."""
+    cfg = LLAMA_1B
+    w = synth_weights(cfg, seed=0)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 512)
+    r = LlamaRunner(ctx, cfg, w)
+    r.prefill(prompt)
+    first = r.logits()
+    r.decode(127)
+    last = r.logits()
+    toks = r.tokens()
+    assert toks.shape == (640,)
+    r.close()
+    ref = ol.forward(cfg, w, toks[:639], first=511)  # positions 511..638
+    tol = 2e-2
+    worst = 0.0
+    for i in range(ref.shape[0]):
+        scale = np.abs(ref[i]).max()
+        assert ref[i][toks[512 + i]] >= ref[i].max() - 2 * tol * scale, f"step {i}: token {toks[512 + i]}"
+    for i, dev in ((0, first), (127, last)):
+        d = np.abs(dev - ref[i]).max() / np.abs(ref[i]).max()
+        worst = max(worst, d)
+        assert d <= tol, f"step {i}: logits rel diff {d:.3e}"
+    print(f"[1B] 128 greedy tokens consistent; logits rel diff (first, last) <= {worst:.3e}", flush=True)
