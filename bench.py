@@ -17,6 +17,10 @@ Printed JSON (one line, stdout):
                    f32 GEMV on the load-time-dequantized f32 weight (oracle port)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
   decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2])
+  swiglu           configs[2]: the fused SwiGLU MLP (gate+up pass, then down)
+                   at the 7B shape, M=1 and M=8, GB/s of its algorithmic bytes
+  decode_tok_s     configs[4]: 1.1B int8 Llama, 512-token prompt, then 128
+                   greedy decode steps timed (HIP events), tokens/s
 
 Algorithmic bytes per GEMV = N*K (codes) + 4*N (scales) + 2*M*K (X) + 2*M*N (Y).
 """
@@ -131,6 +135,72 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     return {"shape": f"{m}x{n}x{k}", "ms": round(ms, 5), "tflops": round(tflops, 2),
             "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+
+
+def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60) -> dict:
+    """y = down(silu(gate.x) * (up.x)), gate/up int8 [11008,4096],
+    down int8 [4096,11008], per-row scales; x fp16 [m,4096].  Bytes per MLP =
+    3*I*H codes + 4*(2I+H) scales + 2mH (x) + 2*2mI (h written, read) + 4mH (y f32)."""
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+    from rusty_amd.hiprt import Event
+
+    I, H = 11008, 4096
+    g = synth.rng(2)
+    mats = [[QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, I, H)),
+             QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, I, H)),
+             QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, H, I))] for _ in range(copies)]
+    x = UnifiedTensor.new(ctx, synth.activations(g, m, H), dtype=DType.FP16)
+    y = UnifiedTensor.empty(ctx, [m, H], DType.FP32)  # |y| ~1e5 at these statistics: past fp16 range
+    h = UnifiedTensor.empty(ctx, [2, m, I], DType.FP16)
+    for i in range(2 * copies):
+        engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h)
+    ctx.sync()
+    a, b = Event(), Event()
+    a.record(ctx.stream)
+    for i in range(launches):
+        engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h)
+    b.record(ctx.stream)
+    b.synchronize()
+    us = a.elapsed_ms(b) / launches * 1e3
+    nbytes = 3 * I * H + 4 * (2 * I + H) + 2 * m * H + 2 * 2 * m * I + 4 * m * H
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"m": m, "us_per_mlp": round(us, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "launches": "gate+up pass, down pass (2 kernels)"}
+
+
+def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2) -> dict:
+    """1.1B int8 Llama greedy decode, one HIP-graph launch per token.
+    Algorithmic bytes per token = int8 codes + f32 scales of every Linear and
+    the lm_head + the fp16 KV cache rows attention reads (positions 0..pos,
+    once per KV head) + one fp16 embedding row."""
+    from rusty_amd.hiprt import Event
+    from rusty_amd.llama import LLAMA_1B, LlamaRunner, synth_weights
+
+    cfg = LLAMA_1B
+    runner = LlamaRunner(ctx, cfg, synth_weights(cfg, seed=0))
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, prompt_len)
+    best = None
+    for _ in range(reps):
+        runner.prefill(prompt)
+        a, b = Event(), Event()
+        a.record(ctx.stream)
+        runner.decode(steps)
+        b.record(ctx.stream)
+        b.synchronize()
+        ms = a.elapsed_ms(b)
+        best = ms if best is None else min(best, ms)
+    toks = runner.tokens()
+    runner.close()
+    kv_row = cfg.n_kv_heads * cfg.head_dim * 2 * 2  # K and V, fp16, one position
+    kv = cfg.n_layers * kv_row * sum(prompt_len + i + 1 for i in range(steps)) / steps
+    per_tok = cfg.weight_bytes() + kv + cfg.hidden * 2
+    tok_s = steps / (best * 1e-3)
+    gbs = per_tok * tok_s / 1e9
+    return {"tok_s": round(tok_s, 1), "ms_per_token": round(best / steps, 4), "bytes_per_token": int(per_tok),
+            "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "config": "1.1B: 22 layers, hidden 2048, 32/4 heads x 64, SwiGLU 5632, vocab 32000; "
+                      f"{prompt_len}-token random prompt, {steps} greedy steps timed, best of {reps}",
+            "generated_head": [int(t) for t in toks[prompt_len:prompt_len + 8]]}
 
 
 def traffic_from_profile(kernel: str):
@@ -249,7 +319,14 @@ def main() -> int:
             pf.append(prefill(ctx, engine, n, k, steps=args.prefill_steps))
             log(f"prefill {pf[-1]}")
         result["prefill"] = pf
-        result["decode_tok_s"] = None  # configs[4] (1.1B decode loop) not built yet
+        sw = [swiglu(ctx, engine, m) for m in (1, 8)]
+        for e in sw:
+            log(f"swiglu {e}")
+        result["swiglu"] = sw
+        dec = decode_loop(ctx)
+        log(f"decode {dec}")
+        result["decode_tok_s"] = dec["tok_s"]
+        result["decode"] = dec
 
     if not args.no_cpu_baseline:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
