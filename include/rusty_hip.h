@@ -163,6 +163,18 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
 int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
                   rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream);
 
+/* Input gradient through a frozen quantized Linear (LoRA fine-tuning):
+ * dX[m, k_in] = dY[m, n_out] . deq(W).  The `grad_a = matmul_bt(grad, b)`
+ * step of MatMulNode::backward (rusty-autograd/src/lib.rs:152-158) with b the
+ * dequantized f32 weight of Linear::forward (rusty-graph/src/lib.rs:69-70);
+ * the weight gradient is not formed.  Computed in f32 (one fma per term in
+ * ascending n_out, W dequantized exactly as rq_qweight_dequantize does), so
+ * with f32 dY and dX the result equals rq_matmul(dY, dequantized W) bit for
+ * bit, without materialising the f32 weight.  dy_dtype/dx_dtype: RQ_F32 or
+ * RQ_F16. */
+int rq_qmatmul_dx(rq_ctx *ctx, const rq_qweight *w, const void *dy, rq_dtype dy_dtype, void *dx, rq_dtype dx_dtype,
+                  int64_t m, rq_stream stream);
+
 /* ---- int8-weight Llama greedy decode ------------------------------------
  * LlamaModel::forward (rusty-graph/src/lib.rs:420-436) over LlamaBlock
  * (:364-378: norm1 -> Attention -> add -> norm2 -> MLP -> add), Attention

@@ -322,4 +322,19 @@ int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, con
     return qmatmul_dispatch(ctx, *down, h, RQ_F16, y, y_dtype, m, s);
 }
 
+int rq_qmatmul_dx(rq_ctx *ctx, const rq_qweight *w, const void *dy, rq_dtype dy_dtype, void *dx, rq_dtype dx_dtype,
+                  int64_t m, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    if ((dy_dtype != RQ_F16 && dy_dtype != RQ_F32) || (dx_dtype != RQ_F16 && dx_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
+    int64_t t;
+    if (!mul_ok(m, w->k_in, &t) || !mul_ok(m, w->n_out, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0 || w->k_in == 0) return RQ_OK;
+    if (!dx || (w->n_out > 0 && !dy)) return fail(RQ_ERR_INVALID_ARGUMENT, "null gradient pointer");
+    return launch_qmatmul_dx(*w, dy, dy_dtype, dx, dx_dtype, m, pick(ctx, stream));
+}
+
 }  // extern "C"

@@ -83,6 +83,9 @@ int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void 
 int launch_swiglu_generic(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h,
                           int64_t m, hipStream_t s);
 int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_t s);
+// dX[m, k_in] = dY[m, n_out] . deq(W), W dequantized while staged (f32 fma, ascending n_out).
+int launch_qmatmul_dx(const rq_qweight &w, const void *dy, rq_dtype dyt, void *dx, rq_dtype dxt, int64_t m,
+                      hipStream_t s);
 
 // Y = X . deq(W)^T over every kernel family, picked by m, dtypes and shape.
 int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,

@@ -302,6 +302,20 @@ class ComputeEngine:
         call("rq_qmatmul", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], out.ptr, _XDT[out.dtype], m,
              _stream(stream))
 
+    def qmatmul_dx(self, ctx: WgpuContext, dy: UnifiedTensor, w: QuantizedTensor, dx: UnifiedTensor,
+                   stream=None) -> None:
+        """Input gradient of ``qmatmul`` with the weight frozen:
+        ``dx[m, k_in] = dy[m, n_out] . deq(w)`` -- the ``grad_a`` of
+        ``MatMulNode::backward`` (rusty-autograd/src/lib.rs:152-158)."""
+        if dy.dtype not in _XDT or dx.dtype not in _XDT:
+            raise ValueError("dy and dx must be FP16 or FP32")
+        m = dy.numel // w.n_out if w.n_out else dx.shape[0]
+        if dy.numel != m * w.n_out or dx.numel != m * w.k_in:
+            raise ValueError(f"dy {dy.shape} / dx {dx.shape} do not match weight [{w.n_out}, {w.k_in}]")
+        d = w.descriptor()
+        call("rq_qmatmul_dx", ctx.handle, ctypes.byref(d), dy.ptr, _XDT[dy.dtype], dx.ptr, _XDT[dx.dtype], m,
+             _stream(stream))
+
     def mlp_swiglu(self, ctx: WgpuContext, x: UnifiedTensor, gate: QuantizedTensor, up: QuantizedTensor,
                    down: QuantizedTensor, out: UnifiedTensor, h: UnifiedTensor | None = None,
                    stream=None) -> UnifiedTensor:

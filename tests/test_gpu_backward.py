@@ -1,0 +1,85 @@
+"""Input gradient through a frozen quantized Linear (rq_qmatmul_dx), GPU.
+
+With f32 dY and dX the result must equal, bit for bit, the oracle's
+k-ascending fused f32 matmul of dY with the oracle-dequantized weight -- the
+reference's `grad_a = matmul_bt(grad, W_f32[in, out])` (MatMulNode::backward,
+rusty-autograd/src/lib.rs:152-158), written in the [out, in] orientation.
+fp16 operands are checked against the f64 truth with the fp16 tolerance
+|d| <= 2e-3*|y| + 2e-3*max|y|.
+"""
+import numpy as np
+import pytest
+
+from conftest import f16_tol_check
+from oracle import oracle as orc
+from rusty_amd import DType, QuantizedTensor, RqError, UnifiedTensor, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("m,n_out,k_in", [(1, 64, 64), (37, 200, 96), (130, 1024, 512), (64, 4096, 1000)])
+@pytest.mark.parametrize("fmt", ["rowwise", "affine"])
+def test_dx_bit_exact_f32(ctx, engine, m, n_out, k_in, fmt):
+    g = synth.rng(m + n_out + k_in)
+    if fmt == "rowwise":
+        q, s = synth.rowwise_weight(g, n_out, k_in)
+        w, wdeq = QuantizedTensor.rowwise(ctx, q, s), orc.rowwise_dequantize(q, s)
+    else:
+        grp = 8 if k_in % 64 else 64
+        u, s, b = synth.affine_weight(g, n_out, k_in, group=grp)
+        w = QuantizedTensor.affine(ctx, u, s, b, group=grp)
+        wdeq = orc.affine_dequantize(u, s, b, group=grp).reshape(n_out, k_in)
+    dy = g.standard_normal((m, n_out), dtype=np.float32)
+    dx = UnifiedTensor.empty(ctx, [m, k_in], DType.FP32)
+    engine.qmatmul_dx(ctx, UnifiedTensor.new(ctx, dy), w, dx)
+    want = orc.matmul(dy, wdeq.reshape(n_out, k_in), fused=True)
+    got = dx.to_vec()
+    assert np.array_equal(bits(got), bits(want)), f"{np.count_nonzero(bits(got) != bits(want))} elements differ"
+
+
+def test_dx_fp16(ctx, engine):
+    g = synth.rng(5)
+    q, s = synth.rowwise_weight(g, 768, 512)
+    w = QuantizedTensor.rowwise(ctx, q, s)
+    dy = synth.activations(g, 50, 768)  # fp16
+    dx = UnifiedTensor.empty(ctx, [50, 512], DType.FP16)
+    engine.qmatmul_dx(ctx, UnifiedTensor.new(ctx, dy, dtype=DType.FP16), w, dx)
+    truth = dy.astype(np.float64) @ (q.astype(np.float64) * s.astype(np.float64)[:, None])
+    max_abs, rel, ok = f16_tol_check(dx.to_vec(), truth)
+    print(f"[dx fp16] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
+def test_dx_is_transpose_of_forward(ctx, engine):
+    # <dy, x . deq(W)^T> == <dy . deq(W), x>: the forward and the input
+    # gradient use the same weight and orientation
+    g = synth.rng(6)
+    q, s = synth.rowwise_weight(g, 300, 256)
+    w = QuantizedTensor.rowwise(ctx, q, s)
+    x = g.standard_normal((20, 256), dtype=np.float32)
+    dy = g.standard_normal((20, 300), dtype=np.float32)
+    y = UnifiedTensor.empty(ctx, [20, 300], DType.FP32)
+    engine.qmatmul(ctx, UnifiedTensor.new(ctx, x), w, y)
+    dx = UnifiedTensor.empty(ctx, [20, 256], DType.FP32)
+    engine.qmatmul_dx(ctx, UnifiedTensor.new(ctx, dy), w, dx)
+    lhs = float(np.sum(dy.astype(np.float64) * y.to_vec()))
+    rhs = float(np.sum(dx.to_vec().astype(np.float64) * x))
+    assert lhs == pytest.approx(rhs, rel=1e-4)
+
+
+def test_dx_errors(ctx, engine):
+    g = synth.rng(7)
+    w = QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, 32, 16))
+    with pytest.raises(ValueError):
+        engine.qmatmul_dx(ctx, UnifiedTensor.empty(ctx, [2, 31]), w, UnifiedTensor.empty(ctx, [2, 16]))
+    from rusty_amd import _lib
+    import ctypes
+    d = w.descriptor()
+    with pytest.raises(RqError, match="RQ_ERR_INVALID_ARGUMENT"):
+        _lib.call("rq_qmatmul_dx", ctx.handle, ctypes.byref(d), None, 0, None, 0, 3, None)
+    with pytest.raises(RqError, match="RQ_ERR_INVALID_ARGUMENT"):
+        _lib.call("rq_qmatmul_dx", ctx.handle, ctypes.byref(d), None, 7, None, 0, 3, None)
