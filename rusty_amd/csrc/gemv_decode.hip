@@ -103,14 +103,19 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     const int row0 = blockIdx.x * ROWS;
 
     // X slice (issued first so its wait does not cover the weight stream).
+    // NORM: the block loads the f32 row and the norm weight once, spread over
+    // all its threads (chunk c by thread c % DT), and shares the normalised
+    // fp16 row through LDS -- not once per row group.
+    constexpr int XC = CPT * TPR;            // chunks the row groups cover
+    constexpr int NL = (XC + DT - 1) / DT;   // NORM: chunks loaded per thread
     uint32_t xh[CPT][M][8];
-    uint4 xf4[NORM ? CPT : 1][4], nw4[NORM ? CPT : 1][2];
+    uint4 xf4[NORM ? NL : 1][4], nw4[NORM ? NL : 1][2];
     if constexpr (NORM) {
         const auto rxf = make_rsrc(Xf, (uint32_t)K * 4u);
         const auto rnw = make_rsrc(NW, (uint32_t)K * 2u);
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = tt + TPR * j;
+        for (int j = 0; j < NL; ++j) {
+            const int c = t + DT * j;
             const uint32_t off = c < C ? (uint32_t)c * 64u : kOOB, offw = c < C ? (uint32_t)c * 32u : kOOB;
 #pragma unroll
             for (int q = 0; q < 4; ++q) xf4[j][q] = bload<0>(rxf, off + 16 * q);
@@ -145,41 +150,54 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             w[r][j] = bload<2>(r < R ? rw : rw2, off);
         }
     if constexpr (NORM) {
-        // sum of squares over row group 0 (each row group holds all of x)
+        // sum of squares of the row (chunks past K loaded as zero), one barrier
         __shared__ float nred[DT / 64];
+        __shared__ uint4 xsh[XC * 2];  // the normalised fp16 row, 2 x 16 B per chunk
         float ss = 0.0f;
-        if (rp == 0) {
 #pragma unroll
-            for (int j = 0; j < CPT; ++j)
+        for (int j = 0; j < NL; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float f[4] = {__builtin_bit_cast(float, xf4[j][q].x), __builtin_bit_cast(float, xf4[j][q].y),
-                                        __builtin_bit_cast(float, xf4[j][q].z), __builtin_bit_cast(float, xf4[j][q].w)};
+            for (int q = 0; q < 4; ++q) {
+                const float f[4] = {__builtin_bit_cast(float, xf4[j][q].x), __builtin_bit_cast(float, xf4[j][q].y),
+                                    __builtin_bit_cast(float, xf4[j][q].z), __builtin_bit_cast(float, xf4[j][q].w)};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-                }
-        }
+                for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+            }
         ss = wave_total(ss);
         if (lane == 0) nred[wave] = ss;
         __syncthreads();
         ss = (nred[0] + nred[1]) + (nred[2] + nred[3]);
         const float inv = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
-        for (int j = 0; j < CPT; ++j)
+        for (int j = 0; j < NL; ++j) {
+            const int c = t + DT * j;
+            if (c >= XC) break;
+            uint32_t hv[8];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint4 xv = xf4[j][q];
                 const float f[4] = {__builtin_bit_cast(float, xv.x), __builtin_bit_cast(float, xv.y),
                                     __builtin_bit_cast(float, xv.z), __builtin_bit_cast(float, xv.w)};
-                // norm weights of elements 4q..4q+3: halves 4q..4q+3 of the 16 in nw4[j]
+                // norm weights of elements 4q..4q+3: halves 4q..4q+3 of the chunk's 16
                 const uint4 nv = nw4[j][q >> 1];
                 const uint32_t n01 = (q & 1) ? nv.z : nv.x, n23 = (q & 1) ? nv.w : nv.y;
                 const h2_t a = __builtin_bit_cast(h2_t, n01), b = __builtin_bit_cast(h2_t, n23);
                 const h2_t lo = {(_Float16)((f[0] * inv) * (float)a.x), (_Float16)((f[1] * inv) * (float)a.y)};
                 const h2_t hi = {(_Float16)((f[2] * inv) * (float)b.x), (_Float16)((f[3] * inv) * (float)b.y)};
-                xh[j][0][2 * q] = __builtin_bit_cast(uint32_t, lo);
-                xh[j][0][2 * q + 1] = __builtin_bit_cast(uint32_t, hi);
+                hv[2 * q] = __builtin_bit_cast(uint32_t, lo);
+                hv[2 * q + 1] = __builtin_bit_cast(uint32_t, hi);
             }
+            xsh[2 * c] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            xsh[2 * c + 1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+            const uint4 a = xsh[2 * c], b = xsh[2 * c + 1];
+            xh[j][0][0] = a.x; xh[j][0][1] = a.y; xh[j][0][2] = a.z; xh[j][0][3] = a.w;
+            xh[j][0][4] = b.x; xh[j][0][5] = b.y; xh[j][0][6] = b.z; xh[j][0][7] = b.w;
+        }
     }
     float sg[R][CPT], bg[R][CPT];
     if constexpr (FMT == 1) {

@@ -43,6 +43,7 @@ struct rq_llama {
     float *x = nullptr, *qkv_out = nullptr, *logits = nullptr;
     _Float16 *attn = nullptr, *h = nullptr, *kc = nullptr, *vc = nullptr;
     int *tokens = nullptr, *pos = nullptr, *n_prompt = nullptr;
+    float2 *rope = nullptr;  // (cos, sin) per position and rotated pair
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
@@ -88,79 +89,89 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
     }
 }
 
-// Threads per attention block: 16 waves for head_dim 64, 8 for 128 (register
-// budget of the in-flight K and V rows).
-template <int HD>
-constexpr int attn_threads() { return HD == 64 ? 1024 : 512; }
-
 // Decode attention of query head blockIdx.x at position pos = *pos_p.
-// RoPE (kernels.wgsl:60-79, rotate-half: dims d and d + HD/2 by the angle
-// pos * theta^(-2d/HD)) is applied to q and to the new key; the block of the
-// first query head of each KV group appends the new key and value (rounded to
-// fp16) to the cache at `pos` (rusty-graph/src/lib.rs:235-246).  Every block
-// uses the fp16-rounded new key/value for position pos and reads the cache
-// only below pos (the buffer resource ends there; rows past it read as zero),
-// so no block reads what another block of this launch writes.
-// Scores q.k / sqrt(HD) over positions 0..pos (causal), softmax in f32,
-// output fp16 [n_heads * HD].  GQA: query head h reads KV head
-// h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
+// RoPE (kernels.wgsl:60-79, rotate-half pairs (d, d + HD/2), angle
+// pos * theta^(-2d/HD) from a (cos, sin) table built once at create) is
+// applied to q and to the new key; the block of the first query head of each
+// KV group appends the new key and value (rounded to fp16) to the cache at
+// `pos` (rusty-graph/src/lib.rs:235-246).  Every block uses the new key/value
+// from LDS for position pos and reads the cache only below pos (the buffer
+// resource ends there; rows past it read as zero), so no block reads what
+// another block of this launch writes.  Scores q.k / sqrt(HD) over positions
+// 0..pos (causal), softmax in f32, output fp16 [n_heads * HD].  GQA: query
+// head h reads KV head h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
 //
-// Memory-latency bound (tens of KB per head), so the loads are shaped for
-// one round trip per pass: a pass covers AT positions, each wave 64
-// consecutive rows (8 or 16 KB contiguous for K and for V); lane l loads
-// 16-byte chunk l % CH of row (i * 64 + l) / CH for i < CH, all K and V loads
-// issued before any is used.  Row scores are finished by xor-shuffles over
-// the CH lanes of a row; P.V partials per lane are summed over the lanes of
-// the same chunk, then over waves in LDS.  Passes beyond the first (pos >= AT)
-// combine by the online-softmax rescale.
+// Latency-bound (tens of KB per head): the first pass's K and V rows are
+// requested right after pos is read, before the RoPE prologue; a pass covers
+// PASS positions, each wave RW consecutive rows (8 KB contiguous for K and for
+// V); lane l holds 16-byte chunk l % CH of row i * RPI + l / CH for i < 8, all
+// in flight before any is used.  Row scores finish with xor-shuffles over the
+// CH lanes of a row; P.V partials are summed over the lanes of a chunk, then
+// over waves in LDS; passes beyond the first (pos >= PASS) combine by the
+// online-softmax rescale.  Measured against a split over positions (one block
+// per 128-position chunk): its cross-block combine needs either device-scope
+// fences (L2 write-back, 3-5x slower) or a second launch, and at a 640-token
+// context both lose to one block per head.
+constexpr int ATT = 1024;  // threads per attention block
+
 template <int HD>
-__global__ __launch_bounds__(attn_threads<HD>()) void k_attn_decode(
-    const float *__restrict__ qkv, _Float16 *__restrict__ kc, _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
-    _Float16 *__restrict__ out, int n_heads, int n_kv, int max_seq, float theta) {
-    constexpr int AT = attn_threads<HD>(), NW = AT / 64;
-    constexpr int CH = HD / 8;    // 16-byte chunks per row
-    constexpr int RPI = 64 / CH;  // rows per wave-wide load
+__global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ qkv, _Float16 *__restrict__ kc,
+                                                     _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
+                                                     const float2 *__restrict__ rope, _Float16 *__restrict__ out,
+                                                     int n_heads, int n_kv, int max_seq) {
+    constexpr int NW = ATT / 64;
+    constexpr int CH = HD / 8;         // 16-byte chunks per row
+    constexpr int RPI = 64 / CH;       // rows per wave-wide load
+    constexpr int NI = 8;              // loads of K (and of V) per lane per pass
+    constexpr int RW = NI * RPI;       // rows per wave per pass
+    constexpr int PASS = NW * RW;      // positions per pass
     constexpr int HALF = HD / 2;
     __shared__ float qs[HD], kn[HD], vn[HD], redm[NW], reds[NW];
     __shared__ float accs[NW][HD];
     const int hd = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int pos = *pos_p;
     const int grp = n_heads / n_kv, g = hd / grp;
+    _Float16 *kcg = kc + (size_t)g * max_seq * HD;
+    _Float16 *vcg = vc + (size_t)g * max_seq * HD;
+    const auto rk = make_rsrc(kcg, (uint32_t)pos * HD * 2u);
+    const auto rv = make_rsrc(vcg, (uint32_t)pos * HD * 2u);
+    const int ch = lane % CH, rl = lane / CH;
+    uint4 kr[NI], vr[NI];
+    auto load_pass = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int row = c0 + RW * w + i * RPI + rl;
+            const uint32_t off = row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
+            kr[i] = bload(rk, off);
+            vr[i] = bload(rv, off);
+        }
+    };
+    load_pass(0);
+
     const float *q = qkv + (size_t)hd * HD;
     const float *k = qkv + (size_t)n_heads * HD + (size_t)g * HD;
     const float *v = qkv + (size_t)(n_heads + n_kv) * HD + (size_t)g * HD;
     if (t < HALF) {
-        const float inv_freq = powf(theta, -2.0f * (float)t / (float)HD);
-        float sn, cs;
-        sincosf((float)pos * inv_freq, &sn, &cs);
+        const float2 cs = rope[(size_t)pos * HALF + t];  // (cos, sin) of pos * theta^(-2t/HD)
         const float q1 = q[t], q2 = q[t + HALF], k1 = k[t], k2 = k[t + HALF];
-        qs[t] = q1 * cs - q2 * sn;
-        qs[t + HALF] = q1 * sn + q2 * cs;
-        kn[t] = (float)(_Float16)(k1 * cs - k2 * sn);
-        kn[t + HALF] = (float)(_Float16)(k1 * sn + k2 * cs);
+        qs[t] = q1 * cs.x - q2 * cs.y;
+        qs[t + HALF] = q1 * cs.y + q2 * cs.x;
+        kn[t] = (float)(_Float16)(k1 * cs.x - k2 * cs.y);
+        kn[t + HALF] = (float)(_Float16)(k1 * cs.y + k2 * cs.x);
     }
     if (t < HD) vn[t] = (float)(_Float16)v[t];
     __syncthreads();
-    _Float16 *kcg = kc + (size_t)g * max_seq * HD;
-    _Float16 *vcg = vc + (size_t)g * max_seq * HD;
     if (hd % grp == 0 && t < HD) {
         kcg[(size_t)pos * HD + t] = (_Float16)kn[t];
         vcg[(size_t)pos * HD + t] = (_Float16)vn[t];
     }
-    const auto rk = make_rsrc(kcg, (uint32_t)pos * HD * 2u);
-    const auto rv = make_rsrc(vcg, (uint32_t)pos * HD * 2u);
-    const int ch = lane % CH, rl = lane / CH;
-    float qv[8], knv[8], vnv[8];
+    float qv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        qv[e] = qs[ch * 8 + e];
-        knv[e] = kn[ch * 8 + e];
-        vnv[e] = vn[ch * 8 + e];
-    }
+    for (int e = 0; e < 8; ++e) qv[e] = qs[ch * 8 + e];
     // score of the new key (position pos), reduced over the CH lanes of a row
     float s_new = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s_new = fmaf(qv[e], knv[e], s_new);
+    for (int e = 0; e < 8; ++e) s_new = fmaf(qv[e], kn[ch * 8 + e], s_new);
 #pragma unroll
     for (int o = 1; o < CH; o <<= 1) s_new += __shfl_xor(s_new, o, 64);
 
@@ -169,29 +180,25 @@ __global__ __launch_bounds__(attn_threads<HD>()) void k_attn_decode(
     float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int c0 = 0; c0 < T; c0 += AT) {
-        const int base = c0 + 64 * w;
-        uint4 kr[CH], vr[CH];
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int row = base + i * RPI + rl;
-            const uint32_t off = row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
-            kr[i] = bload(rk, off);
-            vr[i] = bload(rv, off);
-        }
-        float sv[CH];
+    for (int c0 = 0; c0 < T; c0 += PASS) {
+        const int base = c0 + RW * w;
+        if (c0 > 0) load_pass(c0);  // the first pass was requested before the prologue
+        const bool live = base < T;  // wave-uniform: waves past the context only join the reductions
+        float sv[NI];
         float lm = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            float f[8], s = 0.0f;
+        for (int i = 0; i < NI; ++i) {
+            sv[i] = -__builtin_inff();
+            if (!live) continue;
+            float f[8], sc = 0.0f;
             widen8(kr[i], f);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s = fmaf(qv[e], f[e], s);
+            for (int e = 0; e < 8; ++e) sc = fmaf(qv[e], f[e], sc);
 #pragma unroll
-            for (int o = 1; o < CH; o <<= 1) s += __shfl_xor(s, o, 64);
+            for (int o = 1; o < CH; o <<= 1) sc += __shfl_xor(sc, o, 64);
             const int row = base + i * RPI + rl;
-            s = row == pos ? s_new : s;
-            sv[i] = row < T ? s * scale : -__builtin_inff();
+            sc = row == pos ? s_new : sc;
+            sv[i] = row < T ? sc * scale : -__builtin_inff();
             lm = fmaxf(lm, sv[i]);
         }
         lm = wave_max(lm);
@@ -206,13 +213,18 @@ __global__ __launch_bounds__(attn_threads<HD>()) void k_attn_decode(
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
+        for (int i = 0; i < NI; ++i) {
+            if (!live) break;
             const float p = expf(sv[i] - m_new);
             const int row = base + i * RPI + rl;
             float f[8];
-            widen8(vr[i], f);
+            widen8(vr[i], f);  // the row at pos reads as zero (the resource ends there)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, row == pos ? vnv[e] : f[e], acc[e]);
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, f[e], acc[e]);
+            if (row == pos) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, vn[ch * 8 + e], acc[e]);
+            }
             ls += ch == 0 ? p : 0.0f;  // one lane per row counts it
         }
         ls = wave_sum(ls);
@@ -244,6 +256,19 @@ __global__ __launch_bounds__(attn_threads<HD>()) void k_attn_decode(
 }
 
 constexpr int AT = 1024;
+
+// RoPE table: rope[p * (HD/2) + d] = (cos, sin) of p * theta^(-2d/HD) in f32,
+// the reference's angle formula (kernels.wgsl:63-69), for every position.
+__global__ __launch_bounds__(NT) void k_rope_table(float2 *__restrict__ rope, int max_seq, int hd, float theta) {
+    const int half = hd / 2;
+    const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= (int64_t)max_seq * half) return;
+    const int p = (int)(i / half), d = (int)(i % half);
+    const float inv_freq = powf(theta, -2.0f * (float)d / (float)hd);
+    float sn, cs;
+    sincosf((float)p * inv_freq, &sn, &cs);
+    rope[i] = make_float2(cs, sn);
+}
 
 // Greedy pick + embedding gather, one block.  The step processed the token at
 // position pos = *pos_p.  The next token is the prompt's token pos + 1 while
@@ -340,13 +365,13 @@ int enqueue_step(rq_llama *md, hipStream_t s) {
         if ((st = launch_gemv_decode_norm(L.qkv, md->x, L.attn_norm, c.norm_eps, md->qkv_out, s)) != RQ_OK)
             return st;
         if (c.head_dim == 64)
-            hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads), dim3(attn_threads<64>()), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->attn, c.n_heads,
-                               c.n_kv_heads, c.max_seq, c.rope_theta);
+            hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads), dim3(ATT), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->attn, c.n_heads,
+                               c.n_kv_heads, c.max_seq);
         else
-            hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads), dim3(attn_threads<128>()), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->attn, c.n_heads,
-                               c.n_kv_heads, c.max_seq, c.rope_theta);
+            hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads), dim3(ATT), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->attn, c.n_heads,
+                               c.n_kv_heads, c.max_seq);
         RQ_LAUNCH_CHECK();
         if ((st = launch_gemv_decode_add(L.o, md->attn, md->x, 1, s)) != RQ_OK) return st;
         if ((st = launch_swiglu_decode_norm(L.gate, L.up, md->x, L.mlp_norm, c.norm_eps, md->h, s)) != RQ_OK)
@@ -452,7 +477,8 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
     size_t bytes = L * (pad((size_t)QKV * H) + pad((size_t)QKV * 4));
     bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(QW * 2) + pad(2 * I * 2) +
-             2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4);
+             2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4) +
+             pad((size_t)c.max_seq * (c.head_dim / 2) * sizeof(float2));
     hipError_t e = hipMalloc(&md->owned, bytes);
     if (e != hipSuccess) {
         md->owned = nullptr;
@@ -497,6 +523,18 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     md->tokens = carve<int>(p, (size_t)c.max_seq + 1);
     md->pos = carve<int>(p, 1);
     md->n_prompt = carve<int>(p, 1);
+    md->rope = carve<float2>(p, (size_t)c.max_seq * (c.head_dim / 2));
+
+    {
+        const int64_t n = (int64_t)c.max_seq * (c.head_dim / 2);
+        hipLaunchKernelGGL(k_rope_table, dim3((unsigned)cdiv(n, NT)), dim3(NT), 0, s, md->rope, c.max_seq, c.head_dim,
+                           c.rope_theta);
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            release(md);
+            return fail(RQ_ERR_HIP, "rope table: %s", hipGetErrorString(e));
+        }
+    }
     e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         release(md);
