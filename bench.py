@@ -193,7 +193,7 @@ def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60) -> dict:
             "bytes": nbytes, "launches": "gate+up pass, down pass (2 kernels)"}
 
 
-def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2) -> dict:
+def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False) -> dict:
     """1.1B int8 Llama greedy decode, one HIP-graph launch per token.
     Algorithmic bytes per token = int8 codes + f32 scales of every Linear and
     the lm_head + the fp16 KV cache rows attention reads (positions 0..pos,
@@ -203,6 +203,8 @@ def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2) -> 
 
     cfg = LLAMA_1B
     runner = LlamaRunner(ctx, cfg, synth_weights(cfg, seed=0))
+    if eager:
+        runner.set_graph(False)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, prompt_len)
     best = None
     for _ in range(reps):
@@ -278,6 +280,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every step directly (no HIP graph)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
+    ap.add_argument("--only", choices=["prefill", "swiglu", "decode"],
+                    help="run one extra workload alone, no headline (for profiling runs)")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="decode steps as direct launches instead of one graph per token (for tools that "
+                         "do not trace graphs)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -290,6 +297,20 @@ def main() -> int:
     ctx = WgpuContext(0)
     engine = ComputeEngine(ctx)
     log(f"device 0: {ctx.num_cus} CUs")
+
+    if args.only:
+        out = {"only": args.only}
+        if args.only == "prefill":
+            out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps)
+                              for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
+        elif args.only == "swiglu":
+            out["swiglu"] = [swiglu(ctx, engine, m) for m in (1, 8)]
+        else:
+            out["decode"] = decode_loop(ctx, eager=args.decode_eager)
+        log(f"{out}")
+        ctx.close()
+        print(json.dumps(out), flush=True)
+        return 0
 
     wl = GemvWorkload(ctx, 1, 4096, 4096)
     log("headline: GEMV 4096x4096 M=1, %d rotating copies" % wl.copies)
@@ -348,7 +369,7 @@ def main() -> int:
         for e in sw:
             log(f"swiglu {e}")
         result["swiglu"] = sw
-        dec = decode_loop(ctx)
+        dec = decode_loop(ctx, eager=args.decode_eager)
         log(f"decode {dec}")
         result["decode_tok_s"] = dec["tok_s"]
         result["decode"] = dec
