@@ -84,6 +84,18 @@ def test_gemv_shapes(ctx, engine, m, k):
     assert ok, (max_abs, rel)
 
 
+@pytest.mark.parametrize("n,k", [(16391, 2048), (20000, 1024), (16384, 5632)])
+def test_gemv_tall_weights(ctx, engine, n, k):
+    # n_out >= 16384 at m = 1 runs 8 rows per row group (an lm_head shape);
+    # 16391 leaves a ragged last block
+    g = synth.rng(n + k)
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, 1, k)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok, (max_abs, rel)
+
+
 @pytest.mark.parametrize("k", [1024, 4096, 11008])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_gemv_affine_reference_format(ctx, engine, m, k):
