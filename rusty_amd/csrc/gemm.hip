@@ -51,13 +51,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
 }
 
-// DMA of 16 bytes per lane: LDS[lds_base + 16 * lane] = buffer[voff].  Issued
+// DMA of 16 bytes per lane: LDS[lds_addr + 16 * lane] = buffer[voff], with
+// lds_addr a 32-bit LDS address (uniform across the wave).  Issued
 // as inline asm so the compiler does not turn its conservative LDS-DMA alias
 // tracking into a full vmcnt(0) wait before every LDS read; every reader of a
 // stage waits with an explicit s_waitcnt vmcnt instead.  M0 carries the LDS
 // base (one wait state before the load, as the ISA requires).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void *lds_base, uint32_t voff) {
-    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)lds_base);
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
                  : "s"(l), "v"(voff), "s"(r)
@@ -130,7 +131,9 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, gm, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int t = threadIdx.x, wave = t / 64, lane = t % 64;
+    // the wave index as a uniform (scalar) value: LDS bases and DMA offsets
+    // derived from it stay in SGPRs instead of being re-derived every k-step
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t / 64), lane = t % 64;
     const int wm = wave / 2, wn = wave % 2;
     const int fr = lane % 32, h = lane / 32;
     const int nk = K / 64;
@@ -151,12 +154,18 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
         const int row = (wave * WUW + q) * 16 + lane / 4, s = lane % 4;
         woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 2) & 3)) * 16;
     }
-    auto dma = [&](Stage<BM, BN> &st, int kt) {
+    // LDS address of the ring, taken once: per-stage addresses are then plain
+    // scalar sums (a generic-to-LDS pointer cast in the loop costs a null check
+    // and a readfirstlane per DMA)
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_void *)&ring[0];
+    auto dma = [&](int stage, int kt) {
         const bool live = kt < nk;
+        const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)sizeof(Stage<BM, BN>);
+        const uint32_t sw = sx + (uint32_t)(BM * 128);  // the W tile follows the X tile
 #pragma unroll
-        for (int q = 0; q < XUW; ++q) dma16(rx, st.x + (wave * XUW + q) * 1024, live ? xoff[q] + kt * 128 : kOOB);
+        for (int q = 0; q < XUW; ++q) dma16(rx, sx + (uint32_t)(wave * XUW + q) * 1024u, live ? xoff[q] + kt * 128 : kOOB);
 #pragma unroll
-        for (int q = 0; q < WUW; ++q) dma16(rw, st.w + (wave * WUW + q) * 1024, live ? woff[q] + kt * 64 : kOOB);
+        for (int q = 0; q < WUW; ++q) dma16(rw, sw + (uint32_t)(wave * WUW + q) * 1024u, live ? woff[q] + kt * 64 : kOOB);
     };
 
     floatx16 acc[FN][FM];
@@ -218,7 +227,7 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
         constexpr int U = S % 2 == 0 ? S : 2 * S;
         Frag f[2];
 #pragma unroll
-        for (int j = 0; j < S; ++j) dma(ring[j], j);
+        for (int j = 0; j < S; ++j) dma(j, j);
         ready(Ls1{});
         fetch(ring[0], f[0]);
 #pragma unroll 1
@@ -226,7 +235,7 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 ready(Ls2{});
-                dma(ring[u % S], kt + u + S);
+                dma(u % S, kt + u + S);
                 fetch(ring[(u + 1) % S], f[(u + 1) % 2]);
                 mma(f[u % 2]);
             }
@@ -234,13 +243,13 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
     } else {
         Frag f;
 #pragma unroll
-        for (int j = 0; j < S - 1; ++j) dma(ring[j], j);
+        for (int j = 0; j < S - 1; ++j) dma(j, j);
 #pragma unroll 1
         for (int kt = 0; kt < nk; kt += S) {
 #pragma unroll
             for (int u = 0; u < S; ++u) {
                 ready(Ls2{});
-                dma(ring[(u + S - 1) % S], kt + u + S - 1);
+                dma((u + S - 1) % S, kt + u + S - 1);
                 fetch(ring[u % S], f);
                 mma(f);
             }
