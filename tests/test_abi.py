@@ -46,3 +46,33 @@ def test_struct_layout_matches_header():
     # rq_qweight: 3 pointers, 2 int64, 2 int32 -> 48 bytes, no padding surprises
     assert ctypes.sizeof(_lib.rq_qweight) == 48
     assert _lib.rq_qweight.n_out.offset == 24 and _lib.rq_qweight.format.offset == 40
+
+
+def _build_c_example(tmp_path):
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    exe = tmp_path / "abi_example"
+    subprocess.run([gcc, "-std=c99", "-O2", "-Wall", "-Werror", "-I", str(root / "include"),
+                    str(root / "tests" / "c" / "abi_example.c"), "-L", str(root / "rusty_amd"), "-lrusty_hip",
+                    "-Wl,-rpath," + str(root / "rusty_amd"), "-lm", "-o", str(exe)], check=True)
+    return exe
+
+
+def test_c_client_builds_against_header(tmp_path):
+    """The header is plain C (c99, no HIP or C++ includes) and links to the library."""
+    assert _build_c_example(tmp_path).exists()
+
+
+@pytest.mark.gpu
+def test_c_client_runs(tmp_path):
+    import subprocess
+
+    r = subprocess.run([str(_build_c_example(tmp_path))], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "abi_example: OK" in r.stdout
