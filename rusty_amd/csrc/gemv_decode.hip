@@ -199,6 +199,19 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             xh[j][0][4] = b.x; xh[j][0][5] = b.y; xh[j][0][6] = b.z; xh[j][0][7] = b.w;
         }
     }
+    // Per-row scales of the tasks this wave will finish, requested now so the
+    // epilogue does not wait on a global load after the reduction.
+    constexpr int NTW = (TASKS + DT / 64 - 1) / (DT / 64);  // tasks per wave
+    float srow[NTW], srow2[SWI ? NTW : 1];
+    if constexpr (FMT == 0) {
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            const int rin = (wave + (DT / 64) * i) / M;
+            const bool ok = wave + (DT / 64) * i < TASKS && rin < rows_here;
+            srow[i] = ok ? scales[row0 + rin] : 0.0f;
+            if constexpr (SWI) srow2[i] = ok ? scales2[row0 + rin] : 0.0f;
+        }
+    }
     float sg[R][CPT], bg[R][CPT];
     if constexpr (FMT == 1) {
 #pragma unroll
@@ -273,7 +286,10 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     __syncthreads();
 
     // Each wave finishes whole (row, token) tasks.
-    for (int task = wave; task < TASKS; task += DT / 64) {
+#pragma unroll
+    for (int i_t = 0; i_t < NTW; ++i_t) {
+        const int task = wave + (DT / 64) * i_t;
+        if (task >= TASKS) break;
         float v = 0.0f, v2 = 0.0f;
 #pragma unroll
         for (int i = 0; i < TPR / 64; ++i) v += part[task][lane + 64 * i];
@@ -286,8 +302,8 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
         const int rin = task / M, m = task % M;
         const int row = row0 + rin;
         if (lane == 0 && rin < rows_here && m < m_act) {
-            float y = FMT == 0 ? tot * scales[row] : tot;
-            if constexpr (SWI) y = silu(y) * (tot2 * scales2[row]);
+            float y = FMT == 0 ? tot * srow[i_t] : tot;
+            if constexpr (SWI) y = silu(y) * (tot2 * srow2[i_t]);
             const size_t o = (size_t)m * N + row;
             if (ymode == kYF16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
             else if (ymode == kYAdd) reinterpret_cast<float *>(Yv)[o] += y;
