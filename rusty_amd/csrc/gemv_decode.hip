@@ -212,6 +212,15 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             if constexpr (SWI) srow2[i] = ok ? scales2[row0 + rin] : 0.0f;
         }
     }
+    // y += result: the old values of the residual, requested now for the same reason
+    float yold[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) {
+        const int task = wave + (DT / 64) * i, rin = task / M, m = task % M;
+        yold[i] = (ymode == kYAdd && task < TASKS && rin < rows_here && m < m_act)
+                      ? reinterpret_cast<const float *>(Yv)[(size_t)m * N + row0 + rin]
+                      : 0.0f;
+    }
     float sg[R][CPT], bg[R][CPT];
     if constexpr (FMT == 1) {
 #pragma unroll
@@ -306,7 +315,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             if constexpr (SWI) y = silu(y) * (tot2 * srow2[i_t]);
             const size_t o = (size_t)m * N + row;
             if (ymode == kYF16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
-            else if (ymode == kYAdd) reinterpret_cast<float *>(Yv)[o] += y;
+            else if (ymode == kYAdd) reinterpret_cast<float *>(Yv)[o] = yold[i_t] + y;
             else reinterpret_cast<float *>(Yv)[o] = y;
         }
     }
@@ -315,42 +324,51 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
                           const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int);
 
-// Rows per row group (R).  m = 1: 2, or 8 for tall weights (n_out >= 16384,
-// e.g. an lm_head: fewer blocks, each re-reading the activation row less per
-// weight byte); the SwiGLU pass loads R gate + R up rows, 2 pairs when a row
-// group is at most 128 threads, else 1.  m = 2..4: 4 (SwiGLU: 2 pairs).
-// Measured on the decode shapes (gate/up 5632x2048 + norm: 7.5 -> 6.8 us;
-// lm_head 32000x2048 + norm: 15.7 -> 13.0 us; the rest within 2 %).
-template <int TPR>
-constexpr int swi_pairs_m1() { return TPR <= 128 ? 2 : 1; }
+// A kernel instance and the rows per row group (R) it was compiled for; the
+// grid is derived from the same R.
+struct Decode {
+    DecodeFn fn;
+    int r;
+};
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM>
+constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM>, R}; }
 
-inline int rows_per_group(int mt, bool swi, bool tall, int tpr) {
-    if (mt == 1) return swi ? (tpr <= 128 ? 2 : 1) : (tall ? 8 : 2);
-    return swi ? 2 : 4;
-}
-
+// Rows per row group, measured on MI355X with the weights streamed from HBM:
+//  m = 1:
+//   * SwiGLU pass (R gate + R up rows): 2 pairs; 4 with the fused norm at
+//     row groups of <= 128 threads (gate/up 5632x2048: 6.90 -> 6.69 us;
+//     11008x4096 without norm, 1 -> 2 pairs: 15.4 -> 14.7 us);
+//   * tall weights (n_out >= 16384, e.g. an lm_head): 8 -- fewer blocks, each
+//     re-reading the activation row less per weight byte (32000x2048 + norm:
+//     15.7 -> 13.0 us);
+//   * fused norm at row groups of <= 128 threads: 6 -- the f32 row and the
+//     norm weight (6 B per element) are read by every block, so more rows per
+//     block (qkv 3072x2048 + norm: 3.98 -> 3.59 us);
+//   * two or more chunks per thread (k_in > 4096): 4 (2048x5632: 4.26 -> 4.17 us);
+//   * otherwise 2.
+//  m = 2..4: 4 (SwiGLU: 2 pairs).
 // fmt 2 selects the SwiGLU gate/up pass; norm (m = 1, per-row codes only)
 // the fused RMSNorm prologue.
 template <int M, int CPT, int TPR>
-DecodeFn pick_fmt(int fmt, bool norm, bool tall) {
+Decode pick_fmt(int fmt, bool norm, bool tall) {
     if constexpr (M == 1) {
-        constexpr int RS = swi_pairs_m1<TPR>();
-        if (fmt == 2) return norm ? &k_gemv_decode<1, CPT, TPR, RS, 0, true, true>
-                                  : &k_gemv_decode<1, CPT, TPR, RS, 0, true, false>;
-        if (fmt == 0 && tall) return norm ? &k_gemv_decode<1, CPT, TPR, 8, 0, false, true>
-                                          : &k_gemv_decode<1, CPT, TPR, 8, 0, false, false>;
-        if (norm) return &k_gemv_decode<1, CPT, TPR, 2, 0, false, true>;
-        return fmt == 0 ? &k_gemv_decode<1, CPT, TPR, 2, 0, false, false> : &k_gemv_decode<1, CPT, TPR, 2, 1, false, false>;
+        constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
+        constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
+        constexpr int RP = CPT >= 2 ? 4 : 2;     // plain per-row codes
+        if (fmt == 2) return norm ? inst<1, CPT, TPR, RSN, 0, true, true>() : inst<1, CPT, TPR, 2, 0, true, false>();
+        if (fmt == 0 && tall) return norm ? inst<1, CPT, TPR, 8, 0, false, true>() : inst<1, CPT, TPR, 8, 0, false, false>();
+        if (norm) return inst<1, CPT, TPR, RN, 0, false, true>();
+        return fmt == 0 ? inst<1, CPT, TPR, RP, 0, false, false>() : inst<1, CPT, TPR, 2, 1, false, false>();
     } else {
         (void)norm;
         (void)tall;
-        if (fmt == 2) return &k_gemv_decode<M, CPT, TPR, 2, 0, true, false>;
-        return fmt == 0 ? &k_gemv_decode<M, CPT, TPR, 4, 0, false, false> : &k_gemv_decode<M, CPT, TPR, 4, 1, false, false>;
+        if (fmt == 2) return inst<M, CPT, TPR, 2, 0, true, false>();
+        return fmt == 0 ? inst<M, CPT, TPR, 4, 0, false, false>() : inst<M, CPT, TPR, 4, 1, false, false>();
     }
 }
 
 template <int M, int CPT>
-DecodeFn pick_tpr(int tpr, int fmt, bool norm, bool tall) {
+Decode pick_tpr(int tpr, int fmt, bool norm, bool tall) {
     switch (tpr) {
     case 64: return pick_fmt<M, CPT, 64>(fmt, norm, tall);
     case 128: return pick_fmt<M, CPT, 128>(fmt, norm, tall);
@@ -359,7 +377,7 @@ DecodeFn pick_tpr(int tpr, int fmt, bool norm, bool tall) {
 }
 
 template <int M>
-DecodeFn pick_cpt(int cpt, int tpr, int fmt, bool norm, bool tall) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool norm, bool tall) {
     switch (cpt) {
     case 1: return pick_tpr<M, 1>(tpr, fmt, norm, tall);
     case 2: return pick_tpr<M, 2>(tpr, fmt, norm, tall);
@@ -388,11 +406,11 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     const int fmt = w2 ? 2 : w.format;
     const bool norm = nw != nullptr;
     const bool tall = mt == 1 && !w2 && fmt == 0 && N >= 16384;
-    DecodeFn fn = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm, tall) : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false, false)
-                                                                             : pick_cpt<4>(cpt, tpr, fmt, false, false);
-    const int rows = rows_per_group(mt, w2 != nullptr, tall, tpr) * (DT / tpr);
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm, tall)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false, false) : pick_cpt<4>(cpt, tpr, fmt, false, false);
+    const int rows = d.r * (DT / tpr);
     const int64_t blocks = cdiv(N, rows);
-    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
+    hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
                        w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr,
                        norm ? nullptr : (const _Float16 *)x, norm ? (const float *)x : nullptr, nw, eps, y, ymode, m,
                        (int)N, (int)K, w.group);
