@@ -5,12 +5,15 @@
 // (kernels.wgsl:379-400).  MFMA-bound: 2*M*N*K flops over 1 B/weight + 2 B/act.
 //
 // Design (each choice measured on MI355X):
-//  * Block tile BM tokens x BN features, 64 k per step, 4 waves in 2x2, each
-//    wave (BM/2) x (BN/2) outputs as 32x32 tiles of v_mfma_f32_32x32x16_f16
-//    (the 32x32x16 form keeps the MFMA pipe ~82% busy from one wave per SIMD;
-//    16x16x32 only ~50%).  MFMA A = W (32 features x 16 k), B = X^T (16 k x
-//    32 tokens): a lane's accumulator holds runs of 4 consecutive features of
-//    one token (8-byte fp16 stores).
+//  * Block tile BM tokens x BN features, 64 k per step, NW waves in a
+//    (NW/2) x 2 grid, each wave (BM/(NW/2)) x (BN/2) outputs as 32x32 tiles of
+//    v_mfma_f32_32x32x16_f16 (16x16x32 keeps the MFMA pipe only ~50% busy).
+//    MFMA A = W (32 features x 16 k), B = X^T (16 k x 32 tokens): a lane's
+//    accumulator holds runs of 4 consecutive features of one token (8-byte
+//    fp16 stores).  The 256x128 tile runs 8 waves (two per SIMD, 64x64 each,
+//    251 VGPRs with the accumulators): while one wave of a SIMD waits on its
+//    DMA issue or LDS reads the other issues MFMAs (2048x4096x4096:
+//    80.5 -> 74.6 us against 4 waves of 128x64).
 //  * Staging is direct-to-LDS DMA (buffer_load_dwordx4 ... lds): each wave
 //    moves 1 KiB units from global memory straight into LDS, so tiles never
 //    pass through VGPRs or ds_write (register staging measured ~10% slower,
@@ -39,7 +42,6 @@
 namespace rq {
 namespace {
 
-constexpr int TH = 256;
 constexpr uint32_t kOOB = 0x80000000u;  // any offset past a buffer resource reads zero
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -115,13 +117,14 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
     tn = r / gsize;
 }
 
-template <int BM, int BN, bool PINGPONG, int S>
-__global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
+template <int BM, int BN, bool PINGPONG, int S, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm) {
-    constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
-    constexpr int XUW = BM * 128 / 1024 / 4, WUW = BN * 64 / 1024 / 4;  // 1 KiB DMA units per wave
+    constexpr int WGN = 2, WGM = NW / WGN;  // wave grid: WGM along tokens, WGN along features
+    constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+    constexpr int XUW = BM * 128 / 1024 / NW, WUW = BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
     static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
     static_assert(S >= 3 && S * (BM * 128 + BN * 64) <= 160 * 1024, "ring does not fit in LDS");
     constexpr int NOUT = XUW + WUW;  // DMA ops per wave per k-step
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
     // the wave index as a uniform (scalar) value: LDS bases and DMA offsets
     // derived from it stay in SGPRs instead of being re-derived every k-step
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t / 64), lane = t % 64;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int fr = lane % 32, h = lane / 32;
     const int nk = K / 64;
 
@@ -297,13 +300,13 @@ __global__ __launch_bounds__(TH) void k_gemm_rowwise(const int8_t *__restrict__ 
     }
 }
 
-template <int BM, int BN, bool PINGPONG, int S>
+template <int BM, int BN, bool PINGPONG, int S, int NW>
 int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S>), dim3((unsigned)tiles), dim3(TH), 0, s,
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
                        (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m,
                        (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm);
     RQ_LAUNCH_CHECK();
@@ -326,9 +329,9 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // Measured at M = 2048 (N, K in {4096, 11008}): the 4-stage ring with
     // groups of 4 token panels per XCD beats the 3-stage / token-major order
     // by 5-15%; ping-pong fragments beat single-buffered ones at 128x128 too.
-    if (m <= 64) return launch_tiled<64, 128, false, 3>(w, x, y, yt, m, 1, s);
-    if (m < 1024) return launch_tiled<128, 128, true, 4>(w, x, y, yt, m, 4, s);
-    return launch_tiled<256, 128, true, 4>(w, x, y, yt, m, 4, s);
+    if (m <= 64) return launch_tiled<64, 128, false, 3, 4>(w, x, y, yt, m, 1, s);
+    if (m < 1024) return launch_tiled<128, 128, true, 4, 4>(w, x, y, yt, m, 4, s);
+    return launch_tiled<256, 128, true, 4, 8>(w, x, y, yt, m, 4, s);
 }
 
 }  // namespace rq
