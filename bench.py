@@ -100,6 +100,8 @@ def time_steps(ctx, wl: GemvWorkload, steps: int, warmup: int, use_graph: bool =
                 graph.launch()
                 i += wl.copies
         while i < n:
+            if graph is None and i % wl.copies == 0:  # direct: queue the batch behind a device delay
+                device_delay(ctx, HOST_US_PER_LAUNCH * min(wl.copies, n - i))
             wl.launch(i)
             i += 1
 
@@ -119,7 +121,32 @@ def time_steps(ctx, wl: GemvWorkload, steps: int, warmup: int, use_graph: bool =
     return t0.elapsed_ms(t1)
 
 
-def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5):
+HOST_US_PER_LAUNCH = 80  # generous host cost of one direct launch under a tracer
+
+
+def device_delay(ctx, us: float) -> None:
+    """Queues a bounded device-side wait on the context stream: launches the
+    host issues meanwhile line up behind it and then run back to back."""
+    from rusty_amd import _lib
+
+    _lib.call("rq_device_delay", ctx.handle, int(min(us, 100000)), None)
+
+
+class _Direct:
+    """Stands in for a captured graph: launch() queues a device delay, then
+    issues the calls directly, so they run back to back as from the graph
+    (profiling runs whose tracer does not follow graph launches)."""
+
+    def __init__(self, ctx, fn, launches: int):
+        self.ctx, self.fn, self.launches = ctx, fn, launches
+
+    def launch(self) -> None:
+        device_delay(self.ctx, HOST_US_PER_LAUNCH * self.launches)
+        self.fn()
+
+
+def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5,
+            use_graph: bool = True):
     from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
     from rusty_amd.hiprt import Event, Graph
 
@@ -134,7 +161,8 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
     # the sustained clock, not the ramp out of idle; median of 3 replays.
     for _ in range(warmup):
         engine.qmatmul(ctx, x, w, y)
-    graph = Graph(ctx.stream, lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(steps)])
+    fn = lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(steps)]  # noqa: E731
+    graph = Graph(ctx.stream, fn) if use_graph else _Direct(ctx, fn, steps)
     t_end = time.perf_counter() + 0.25
     while time.perf_counter() < t_end:
         graph.launch()
@@ -153,7 +181,7 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
             "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
 
 
-def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60) -> dict:
+def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60, use_graph: bool = True) -> dict:
     """y = down(silu(gate.x) * (up.x)), gate/up int8 [11008,4096],
     down int8 [4096,11008], per-row scales; x fp16 [m,4096].  Bytes per MLP =
     3*I*H codes + 4*(2I+H) scales + 2mH (x) + 2*2mI (h written, read) + 4mH (y f32)."""
@@ -172,8 +200,8 @@ def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60) -> dict:
         engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h)
     # replayed from a HIP graph (no host call between MLPs), after >= 0.25 s
     # of warm-up replays; median of 3 timed replays
-    graph = Graph(ctx.stream, lambda: [engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h)
-                                       for i in range(launches)])
+    fn = lambda: [engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h) for i in range(launches)]  # noqa: E731
+    graph = Graph(ctx.stream, fn) if use_graph else _Direct(ctx, fn, 2 * launches)
     t_end = time.perf_counter() + 0.25
     while time.perf_counter() < t_end:
         graph.launch()
@@ -278,7 +306,9 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-graph", action="store_true", help="launch every step directly (no HIP graph)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
+                         "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
     ap.add_argument("--only", choices=["prefill", "swiglu", "decode"],
                     help="run one extra workload alone, no headline (for profiling runs)")
@@ -289,7 +319,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X and has no "
-              "multi-GPU mode (see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+              "multi-GPU mode (the path would shard along the weight's output rows, one shard per GPU). "
+              "Run with --gpus 1.", file=sys.stderr)
         return 2
 
     from rusty_amd import ComputeEngine, WgpuContext
@@ -301,10 +332,10 @@ def main() -> int:
     if args.only:
         out = {"only": args.only}
         if args.only == "prefill":
-            out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps)
+            out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph)
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
         elif args.only == "swiglu":
-            out["swiglu"] = [swiglu(ctx, engine, m) for m in (1, 8)]
+            out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
         else:
             out["decode"] = decode_loop(ctx, eager=args.decode_eager)
         log(f"{out}")
@@ -337,7 +368,8 @@ def main() -> int:
         "config": {"workload": "configs[1]: decode dequant-GEMV W int8 [4096,4096] per-row f32 scale, "
                                "X fp16 [1,4096], Y fp16; 48 rotating weight copies (806 MB > 2x MALL)",
                    "m": 1, "n": 4096, "k": 4096, "bytes_per_step": wl.bytes,
-                   "launch": "direct" if args.no_graph else "HIP graph of 48 launches"},
+                   "launch": ("direct, batches of 48 queued behind a device delay (for tracers; the timed "
+                              "region includes the delays)") if args.no_graph else "HIP graph of 48 launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile("k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>"),

@@ -77,6 +77,13 @@ int rq_ctx_stream(rq_ctx *ctx, rq_stream *out);
 int rq_ctx_num_cus(rq_ctx *ctx, int *out);
 /* Blocks until all work on `stream` is done (device.poll(Wait), lib.rs:232). */
 int rq_sync(rq_ctx *ctx, rq_stream stream);
+/* A bounded device-side delay: one wave waits on the device's constant-rate
+ * wall clock for `microseconds` (at most 100000, else RQ_ERR_INVALID_ARGUMENT)
+ * and exits.  No counterpart in the reference: a benchmarking aid for drivers
+ * that issue launches one at a time (e.g. under a tracer that does not follow
+ * graph launches) -- work enqueued behind the delay queues up on the device and
+ * then runs back to back, as it does when replayed from a graph. */
+int rq_device_delay(rq_ctx *ctx, uint32_t microseconds, rq_stream stream);
 /* Human-readable name of a status code, and the calling thread's last error
  * message (empty string if none). */
 const char *rq_status_string(int status);

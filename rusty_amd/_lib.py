@@ -88,6 +88,7 @@ _SIGNATURES = {
     "rq_ctx_stream": [_P, POINTER(c_void_p)],
     "rq_ctx_num_cus": [_P, POINTER(c_int)],
     "rq_sync": [_P, _P],
+    "rq_device_delay": [_P, c_uint32, _P],
     "rq_status_string": [c_int],
     "rq_last_error": [],
     "rq_alloc": [_P, c_size_t, POINTER(c_void_p)],

@@ -55,6 +55,13 @@ int rq::check_qweight(const rq_qweight *w) {
     return RQ_OK;
 }
 
+// One wave waits on the device's constant-rate wall clock (wall_clock64,
+// `ticks` periods) and exits; s_sleep between reads keeps the wave idle.
+__global__ void k_device_delay(uint64_t ticks) {
+    const uint64_t t0 = wall_clock64();
+    while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(32);
+}
+
 extern "C" {
 
 const char *rq_status_string(int status) {
@@ -129,6 +136,18 @@ int rq_ctx_num_cus(rq_ctx *ctx, int *out) {
 int rq_sync(rq_ctx *ctx, rq_stream stream) {
     RQ_ENTER(ctx);
     RQ_HIP_TRY(hipStreamSynchronize(pick(ctx, stream)));
+    return RQ_OK;
+}
+
+int rq_device_delay(rq_ctx *ctx, uint32_t microseconds, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (microseconds > 100000u) return fail(RQ_ERR_INVALID_ARGUMENT, "delay of %u us is above 100000 us", microseconds);
+    if (microseconds == 0) return RQ_OK;
+    int khz = 0;  // wall clock rate in kHz (100 MHz on gfx9)
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device) != hipSuccess || khz <= 0) khz = 100000;
+    const uint64_t ticks = (uint64_t)microseconds * (uint64_t)khz / 1000u;
+    hipLaunchKernelGGL(k_device_delay, dim3(1), dim3(64), 0, pick(ctx, stream), ticks);
+    RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 

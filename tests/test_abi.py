@@ -37,6 +37,7 @@ def test_null_arguments_rejected_without_device():
     lib = _lib.lib()
     assert lib.rq_ctx_create(0, None) == _lib.RQ_ERR_INVALID_ARGUMENT
     assert lib.rq_sync(None, None) == _lib.RQ_ERR_INVALID_ARGUMENT
+    assert lib.rq_device_delay(None, 10, None) == _lib.RQ_ERR_INVALID_ARGUMENT
     assert b"null context" in lib.rq_last_error()
     assert lib.rq_qmatmul(None, None, None, 0, None, 0, 1, None) == _lib.RQ_ERR_INVALID_ARGUMENT
     assert lib.rq_ctx_destroy(None) == _lib.RQ_OK
