@@ -81,16 +81,22 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // xn = fp16((x * inv) * nw), inv = 1 / sqrt(mean(x^2) + eps).  Each block
 // reduces the sum of squares itself (one barrier) after its weight loads are
 // in flight, so the norm costs no launch and hides under the weight stream.
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM>
+// SA > 0 (m = 1): the activation row is decode attention's output, combined
+// in the prologue from SA partial softmaxes per head (the attention kernel's
+// split over positions): Xf holds acc[head][SA][attn_hd] (f32) followed by
+// (m, l)[head][SA] (float2); x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
+// M = max_s m_s, rounded to fp16 and shared through LDS like the norm's row.
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
                                                     const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                     const _Float16 *__restrict__ X, const float *__restrict__ Xf,
                                                     const _Float16 *__restrict__ NW, float eps,
                                                     void *__restrict__ Yv, int ymode, int m_act, int N, int K,
-                                                    int group) {
+                                                    int group, int attn_hd) {
     static_assert(!SWI || FMT == 0, "SwiGLU pass is rowwise only");
     static_assert(!NORM || M == 1, "the fused norm serves one activation row");
+    static_assert(SA == 0 || (M == 1 && !NORM && !SWI), "the attention combine serves one activation row");
     constexpr int RP = DT / TPR;
     constexpr int ROWS = R * RP;
     constexpr int TASKS = ROWS * M;
@@ -110,7 +116,31 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     constexpr int NL = (XC + DT - 1) / DT;   // NORM: chunks loaded per thread
     uint32_t xh[CPT][M][8];
     uint4 xf4[NORM ? NL : 1][4], nw4[NORM ? NL : 1][2];
-    if constexpr (NORM) {
+    // SA: 8-element pieces of the row, piece u by thread u % DT: SA (m, l)
+    // pairs of its head and SA x 8 accumulator values
+    constexpr int NU = (2 * XC + DT - 1) / DT;
+    constexpr int SAL = SA > 0 ? SA : 1;
+    uint4 pacc[SA > 0 ? NU : 1][SAL][2], pml[SA > 0 ? NU : 1][(SAL + 1) / 2];
+    if constexpr (SA > 0) {
+        const int nh = K / attn_hd;
+        const auto racc = make_rsrc(Xf, (uint32_t)nh * SA * (uint32_t)attn_hd * 4u);
+        const auto rml = make_rsrc(Xf + (size_t)nh * SA * attn_hd, (uint32_t)nh * SA * 8u);
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = t + DT * j;
+            const bool live = u < 2 * C;
+            const int e0 = u * 8, h = e0 / attn_hd, d0 = e0 - h * attn_hd;
+#pragma unroll
+            for (int q = 0; q < (SAL + 1) / 2; ++q)
+                pml[j][q] = bload<0>(rml, live ? (uint32_t)(h * SA + 2 * q) * 8u : kOOB);
+#pragma unroll
+            for (int sp = 0; sp < SAL; ++sp) {
+                const uint32_t off = live ? ((uint32_t)(h * SA + sp) * attn_hd + d0) * 4u : kOOB;
+                pacc[j][sp][0] = bload<0>(racc, off);
+                pacc[j][sp][1] = bload<0>(racc, off + 16);
+            }
+        }
+    } else if constexpr (NORM) {
         const auto rxf = make_rsrc(Xf, (uint32_t)K * 4u);
         const auto rnw = make_rsrc(NW, (uint32_t)K * 2u);
 #pragma unroll
@@ -149,6 +179,57 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             const uint32_t off = c < C ? (uint32_t)((r % R) * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
             w[r][j] = bload<2>(r < R ? rw : rw2, off);
         }
+    if constexpr (SA > 0) {
+        __shared__ uint4 xsa[XC * 2];  // the combined fp16 row, 2 x 16 B per chunk
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = t + DT * j;
+            if (u >= 2 * XC) break;
+            float mv[SAL], lv[SAL];
+#pragma unroll
+            for (int sp = 0; sp < SAL; ++sp) {
+                const uint4 v = pml[j][sp / 2];
+                mv[sp] = __builtin_bit_cast(float, (sp & 1) ? v.z : v.x);
+                lv[sp] = __builtin_bit_cast(float, (sp & 1) ? v.w : v.y);
+            }
+            float mx = mv[0];
+#pragma unroll
+            for (int sp = 1; sp < SAL; ++sp) mx = fmaxf(mx, mv[sp]);
+            float wgt[SAL], den = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < SAL; ++sp) {
+                wgt[sp] = expf(mv[sp] - mx);  // an empty split's m = -inf weighs 0
+                den = __builtin_fmaf(wgt[sp], lv[sp], den);
+            }
+            const float inv = 1.0f / den;
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < SAL; ++sp) {
+                const uint4 a = pacc[j][sp][0], b = pacc[j][sp][1];
+                const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wgt[sp], __builtin_bit_cast(float, wd[e]), o[e]);
+            }
+            uint32_t hv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const h2_t pr = {(_Float16)(o[2 * q] * inv), (_Float16)(o[2 * q + 1] * inv)};
+                hv[q] = __builtin_bit_cast(uint32_t, pr);
+            }
+            // pieces past the row (chunks the row groups cover beyond K) hold zeros
+            xsa[u] = u < 2 * C ? make_uint4(hv[0], hv[1], hv[2], hv[3]) : make_uint4(0, 0, 0, 0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+            const uint4 a = xsa[2 * c], b = xsa[2 * c + 1];
+            xh[j][0][0] = a.x; xh[j][0][1] = a.y; xh[j][0][2] = a.z; xh[j][0][3] = a.w;
+            xh[j][0][4] = b.x; xh[j][0][5] = b.y; xh[j][0][6] = b.z; xh[j][0][7] = b.w;
+        }
+    }
     if constexpr (NORM) {
         // sum of squares of the row (chunks past K loaded as zero), one barrier
         __shared__ float nred[DT / 64];
@@ -322,7 +403,8 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 }
 
 using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
-                          const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int);
+                          const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int,
+                          int);
 
 // A kernel instance and the rows per row group (R) it was compiled for; the
 // grid is derived from the same R.
@@ -330,8 +412,8 @@ struct Decode {
     DecodeFn fn;
     int r;
 };
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM>
-constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM>, R}; }
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0>
+constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM, SA>, R}; }
 
 // Rows per row group, measured on MI355X with the weights streamed from HBM:
 //  m = 1:
@@ -347,14 +429,20 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM>
 //   * two or more chunks per thread (k_in > 4096): 4 (2048x5632: 4.26 -> 4.17 us);
 //   * otherwise 2.
 //  m = 2..4: 4 (SwiGLU: 2 pairs).
+//   * attention-combine prologue: 4 (each block re-reads the partials, so
+//     fewer, larger blocks).
 // fmt 2 selects the SwiGLU gate/up pass; norm (m = 1, per-row codes only)
-// the fused RMSNorm prologue.
+// the fused RMSNorm prologue; sa (m = 1, per-row codes) the attention combine
+// of sa partials per head.
 template <int M, int CPT, int TPR>
-Decode pick_fmt(int fmt, bool norm, bool tall) {
+Decode pick_fmt(int fmt, bool norm, bool tall, int sa) {
     if constexpr (M == 1) {
         constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
         constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
         constexpr int RP = CPT >= 2 ? 4 : 2;     // plain per-row codes
+        if (sa == 1) return inst<1, CPT, TPR, 4, 0, false, false, 1>();
+        if (sa == 2) return inst<1, CPT, TPR, 4, 0, false, false, 2>();
+        if (sa == 4) return inst<1, CPT, TPR, 4, 0, false, false, 4>();
         if (fmt == 2) return norm ? inst<1, CPT, TPR, RSN, 0, true, true>() : inst<1, CPT, TPR, 2, 0, true, false>();
         if (fmt == 0 && tall) return norm ? inst<1, CPT, TPR, 8, 0, false, true>() : inst<1, CPT, TPR, 8, 0, false, false>();
         if (norm) return inst<1, CPT, TPR, RN, 0, false, true>();
@@ -362,36 +450,38 @@ Decode pick_fmt(int fmt, bool norm, bool tall) {
     } else {
         (void)norm;
         (void)tall;
+        (void)sa;
         if (fmt == 2) return inst<M, CPT, TPR, 2, 0, true, false>();
         return fmt == 0 ? inst<M, CPT, TPR, 4, 0, false, false>() : inst<M, CPT, TPR, 4, 1, false, false>();
     }
 }
 
 template <int M, int CPT>
-Decode pick_tpr(int tpr, int fmt, bool norm, bool tall) {
+Decode pick_tpr(int tpr, int fmt, bool norm, bool tall, int sa) {
     switch (tpr) {
-    case 64: return pick_fmt<M, CPT, 64>(fmt, norm, tall);
-    case 128: return pick_fmt<M, CPT, 128>(fmt, norm, tall);
-    default: return pick_fmt<M, CPT, 256>(fmt, norm, tall);
+    case 64: return pick_fmt<M, CPT, 64>(fmt, norm, tall, sa);
+    case 128: return pick_fmt<M, CPT, 128>(fmt, norm, tall, sa);
+    default: return pick_fmt<M, CPT, 256>(fmt, norm, tall, sa);
     }
 }
 
 template <int M>
-Decode pick_cpt(int cpt, int tpr, int fmt, bool norm, bool tall) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool norm, bool tall, int sa) {
     switch (cpt) {
-    case 1: return pick_tpr<M, 1>(tpr, fmt, norm, tall);
-    case 2: return pick_tpr<M, 2>(tpr, fmt, norm, tall);
-    case 3: return pick_tpr<M, 3>(tpr, fmt, norm, tall);
-    default: return pick_tpr<M, 4>(tpr, fmt, norm, tall);
+    case 1: return pick_tpr<M, 1>(tpr, fmt, norm, tall, sa);
+    case 2: return pick_tpr<M, 2>(tpr, fmt, norm, tall, sa);
+    case 3: return pick_tpr<M, 3>(tpr, fmt, norm, tall, sa);
+    default: return pick_tpr<M, 4>(tpr, fmt, norm, tall, sa);
     }
 }
 
 }  // namespace
 
 // x: fp16 activations, or (nw != null, m = 1) the f32 row to RMS-normalise
-// with the fp16 weight nw and epsilon eps.
+// with the fp16 weight nw and epsilon eps, or (sa > 0, m = 1) the attention
+// partials to combine (sa per head of attn_hd elements).
 static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, const _Float16 *nw, float eps,
-                         void *y, int ymode, int m, hipStream_t s) {
+                         void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0) {
     const int64_t N = w.n_out, K = w.k_in;
     if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
         !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && w.group % 16 != 0))
@@ -399,6 +489,9 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     if (w2 && (w.format != RQ_Q_ROWWISE_I8 || w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16)))
         return RQ_ERR_UNSUPPORTED;
     if (nw && (m != 1 || w.format != RQ_Q_ROWWISE_I8 || !aligned(nw, 16))) return RQ_ERR_UNSUPPORTED;
+    if (sa && (m != 1 || w2 || nw || w.format != RQ_Q_ROWWISE_I8 || (sa != 1 && sa != 2 && sa != 4) ||
+               attn_hd < 8 || attn_hd % 8 != 0 || K % attn_hd != 0))
+        return RQ_ERR_UNSUPPORTED;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
     const int cpt = (int)cdiv(C, tpr);
@@ -406,14 +499,16 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     const int fmt = w2 ? 2 : w.format;
     const bool norm = nw != nullptr;
     const bool tall = mt == 1 && !w2 && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm, tall)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false, false) : pick_cpt<4>(cpt, tpr, fmt, false, false);
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm, tall, sa)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false, false, 0)
+                                       : pick_cpt<4>(cpt, tpr, fmt, false, false, 0);
+    const bool fx = norm || sa;  // x is an f32 source read by the prologue
     const int rows = d.r * (DT / tpr);
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
                        w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr,
-                       norm ? nullptr : (const _Float16 *)x, norm ? (const float *)x : nullptr, nw, eps, y, ymode, m,
-                       (int)N, (int)K, w.group);
+                       fx ? nullptr : (const _Float16 *)x, fx ? (const float *)x : nullptr, nw, eps, y, ymode, m,
+                       (int)N, (int)K, w.group, attn_hd);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
@@ -438,6 +533,11 @@ int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const voi
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
                               float eps, void *h, hipStream_t s) {
     return launch_decode(gate, &up, x, nw, eps, h, kYF16, 1, s);
+}
+
+int launch_gemv_decode_attn_add(const rq_qweight &w, const float *partials, int n_split, int head_dim, float *y,
+                                hipStream_t s) {
+    return launch_decode(w, nullptr, partials, nullptr, 0.0f, y, kYAdd, 1, s, n_split, head_dim);
 }
 
 }  // namespace rq

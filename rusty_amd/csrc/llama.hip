@@ -7,8 +7,11 @@
 //                                                 in its prologue (q, k, v
 //                                                 packed into one weight)
 //   attn = softmax(rope(q) . K^T / sqrt(d)) . V   k_attn_decode (RoPE, KV
-//                                                 append, GQA attention)
-//   x   += attn . Wo^T                            decode GEMV, add epilogue
+//                                                 append, GQA attention, split
+//                                                 over positions: partials)
+//   x   += attn . Wo^T                            decode GEMV: the partials are
+//                                                 combined in its prologue, add
+//                                                 epilogue
 //   h    = silu(xn . Wg^T) * (xn . Wu^T),         fused gate/up decode GEMV,
 //          xn = rmsnorm(x, mlp_norm)              norm in its prologue
 //   x   += h . Wd^T                               decode GEMV, add epilogue
@@ -41,7 +44,9 @@ struct rq_llama {
     rq_qweight lm_head{};
     void *owned = nullptr;  // packed qkv weights + step state, one allocation
     float *x = nullptr, *qkv_out = nullptr, *logits = nullptr;
-    _Float16 *attn = nullptr, *h = nullptr, *kc = nullptr, *vc = nullptr;
+    float *part = nullptr;  // attention partials: acc [n_heads][n_split][head_dim], then (m, l) pairs
+    int n_split = 1;        // attention blocks per query head
+    _Float16 *h = nullptr, *kc = nullptr, *vc = nullptr;
     int *tokens = nullptr, *pos = nullptr, *n_prompt = nullptr;
     float2 *rope = nullptr;  // (cos, sin) per position and rotated pair
     hipGraph_t graph = nullptr;
@@ -89,36 +94,44 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
     }
 }
 
-// Decode attention of query head blockIdx.x at position pos = *pos_p.
+// Decode attention at position pos = *pos_p, split over positions: block
+// (head hd, split sp) of a grid of n_heads * S covers positions [r0, r1) of
+// 0..pos, P = ceil((pos + 1) / S) positions per split, and writes its partial
+// softmax -- the running max m, the sum l of exp(score - m) and the
+// unnormalised accumulator acc[d] = sum exp(score - m) * v[d] -- to
+// part[(hd * S + sp) * HD + d] and ml[hd * S + sp] = (m, l).  An empty range
+// (pos + 1 < S) writes (-inf, 0, 0).  The consumer (the o-projection GEMV's
+// prologue) combines the S partials of a head: out = sum_s e^(m_s - M) acc_s /
+// sum_s e^(m_s - M) l_s, M = max_s m_s.
+//
 // RoPE (kernels.wgsl:60-79, rotate-half pairs (d, d + HD/2), angle
 // pos * theta^(-2d/HD) from a (cos, sin) table built once at create) is
-// applied to q and to the new key; the block of the first query head of each
-// KV group appends the new key and value (rounded to fp16) to the cache at
-// `pos` (rusty-graph/src/lib.rs:235-246).  Every block uses the new key/value
-// from LDS for position pos and reads the cache only below pos (the buffer
-// resource ends there; rows past it read as zero), so no block reads what
-// another block of this launch writes.  Scores q.k / sqrt(HD) over positions
-// 0..pos (causal), softmax in f32, output fp16 [n_heads * HD].  GQA: query
-// head h reads KV head h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
+// applied to q and to the new key; the block that holds position pos in the
+// first query head of each KV group appends the new key and value (rounded
+// to fp16) to the cache at `pos` (rusty-graph/src/lib.rs:235-246).  Every
+// block uses the new key/value from LDS for position pos and reads the cache
+// only below pos (the buffer resource ends there; rows past it read as zero),
+// so no block reads what another block of this launch writes.  Scores
+// q.k / sqrt(HD), softmax in f32.  GQA: query head h reads KV head
+// h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
 //
-// Latency-bound (tens of KB per head): the first pass's K and V rows are
-// requested right after pos is read, before the RoPE prologue; a pass covers
-// PASS positions, each wave RW consecutive rows (8 KB contiguous for K and for
-// V); lane l holds 16-byte chunk l % CH of row i * RPI + l / CH for i < 8, all
-// in flight before any is used.  Row scores finish with xor-shuffles over the
-// CH lanes of a row; P.V partials are summed over the lanes of a chunk, then
-// over waves in LDS; passes beyond the first (pos >= PASS) combine by the
-// online-softmax rescale.  Measured against a split over positions (one block
-// per 128-position chunk): its cross-block combine needs either device-scope
-// fences (L2 write-back, 3-5x slower) or a second launch, and at a 640-token
-// context both lose to one block per head.
-constexpr int ATT = 1024;  // threads per attention block
+// Latency-bound: each block streams its range's K and V rows (2 * P * HD * 2
+// bytes) through one CU, so splitting a head's context over S blocks divides
+// that stream; the first pass's rows are requested right after pos is read,
+// before the RoPE prologue.  A pass covers PASS positions, each wave RW
+// consecutive rows; lane l holds 16-byte chunk l % CH of row i * RPI + l / CH
+// for i < 8, all in flight before any is used.  Row scores finish with
+// xor-shuffles over the CH lanes of a row; P.V partials are summed over the
+// lanes of a chunk, then over waves in LDS; passes beyond the first combine by
+// the online-softmax rescale.
+constexpr int ATT = 256;  // threads per attention block
 
 template <int HD>
 __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ qkv, _Float16 *__restrict__ kc,
                                                      _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
-                                                     const float2 *__restrict__ rope, _Float16 *__restrict__ out,
-                                                     int n_heads, int n_kv, int max_seq) {
+                                                     const float2 *__restrict__ rope, float *__restrict__ part,
+                                                     float2 *__restrict__ ml, int n_heads, int n_kv, int max_seq,
+                                                     int S) {
     constexpr int NW = ATT / 64;
     constexpr int CH = HD / 8;         // 16-byte chunks per row
     constexpr int RPI = 64 / CH;       // rows per wave-wide load
@@ -128,8 +141,10 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     constexpr int HALF = HD / 2;
     __shared__ float qs[HD], kn[HD], vn[HD], redm[NW], reds[NW];
     __shared__ float accs[NW][HD];
-    const int hd = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int hd = blockIdx.x / S, sp = blockIdx.x % S, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int pos = *pos_p;
+    const int T = pos + 1, P = (T + S - 1) / S;
+    const int r0 = min(T, sp * P), r1 = min(T, r0 + P);  // this block's positions [r0, r1)
     const int grp = n_heads / n_kv, g = hd / grp;
     _Float16 *kcg = kc + (size_t)g * max_seq * HD;
     _Float16 *vcg = vc + (size_t)g * max_seq * HD;
@@ -141,12 +156,12 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int row = c0 + RW * w + i * RPI + rl;
-            const uint32_t off = row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
+            const uint32_t off = row < r1 && row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
             kr[i] = bload(rk, off);
             vr[i] = bload(rv, off);
         }
     };
-    load_pass(0);
+    load_pass(r0);
 
     const float *q = qkv + (size_t)hd * HD;
     const float *k = qkv + (size_t)n_heads * HD + (size_t)g * HD;
@@ -161,7 +176,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     }
     if (t < HD) vn[t] = (float)(_Float16)v[t];
     __syncthreads();
-    if (hd % grp == 0 && t < HD) {
+    if (hd % grp == 0 && r1 == T && r0 < r1 && t < HD) {
         kcg[(size_t)pos * HD + t] = (_Float16)kn[t];
         vcg[(size_t)pos * HD + t] = (_Float16)vn[t];
     }
@@ -176,14 +191,13 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     for (int o = 1; o < CH; o <<= 1) s_new += __shfl_xor(s_new, o, 64);
 
     const float scale = 1.0f / sqrtf((float)HD);
-    const int T = pos + 1;
     float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int c0 = 0; c0 < T; c0 += PASS) {
+    for (int c0 = r0; c0 < r1; c0 += PASS) {
         const int base = c0 + RW * w;
-        if (c0 > 0) load_pass(c0);  // the first pass was requested before the prologue
-        const bool live = base < T;  // wave-uniform: waves past the context only join the reductions
+        if (c0 > r0) load_pass(c0);  // the first pass was requested before the prologue
+        const bool live = base < r1;  // wave-uniform: waves past the range only join the reductions
         float sv[NI];
         float lm = -__builtin_inff();
 #pragma unroll
@@ -198,7 +212,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
             for (int o = 1; o < CH; o <<= 1) sc += __shfl_xor(sc, o, 64);
             const int row = base + i * RPI + rl;
             sc = row == pos ? s_new : sc;
-            sv[i] = row < T ? sc * scale : -__builtin_inff();
+            sv[i] = row < r1 ? sc * scale : -__builtin_inff();
             lm = fmaxf(lm, sv[i]);
         }
         lm = wave_max(lm);
@@ -207,7 +221,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
         float cm = redm[0];
 #pragma unroll
         for (int i = 1; i < NW; ++i) cm = fmaxf(cm, redm[i]);
-        const float m_new = fmaxf(m_run, cm);  // finite: row 0 is in the first pass
+        const float m_new = fmaxf(m_run, cm);  // finite: row r0 is in the first pass
         const float alpha = expf(m_run - m_new);
         float ls = 0.0f;
 #pragma unroll
@@ -218,7 +232,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
             const float p = expf(sv[i] - m_new);
             const int row = base + i * RPI + rl;
             float f[8];
-            widen8(vr[i], f);  // the row at pos reads as zero (the resource ends there)
+            widen8(vr[i], f);  // rows at pos and past the range read as zero
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, f[e], acc[e]);
             if (row == pos) {
@@ -247,12 +261,14 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
         for (int e = 0; e < 8; ++e) accs[w][ch * 8 + e] = acc[e];
     }
     __syncthreads();
+    const size_t slot = (size_t)hd * S + sp;
     if (t < HD) {
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < NW; ++i) sum += accs[i][t];
-        out[(size_t)hd * HD + t] = (_Float16)(sum / l_run);
+        part[slot * HD + t] = sum;
     }
+    if (t == 0) ml[slot] = make_float2(m_run, l_run);
 }
 
 constexpr int AT = 1024;
@@ -364,16 +380,18 @@ int enqueue_step(rq_llama *md, hipStream_t s) {
         const rq_llama::Layer &L = md->layers[l];
         if ((st = launch_gemv_decode_norm(L.qkv, md->x, L.attn_norm, c.norm_eps, md->qkv_out, s)) != RQ_OK)
             return st;
+        const int S = md->n_split;
+        float2 *ml = reinterpret_cast<float2 *>(md->part + (size_t)c.n_heads * S * c.head_dim);
         if (c.head_dim == 64)
-            hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads), dim3(ATT), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->attn, c.n_heads,
-                               c.n_kv_heads, c.max_seq);
+            hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads * S), dim3(ATT), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->part, ml,
+                               c.n_heads, c.n_kv_heads, c.max_seq, S);
         else
-            hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads), dim3(ATT), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->attn, c.n_heads,
-                               c.n_kv_heads, c.max_seq);
+            hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads * S), dim3(ATT), 0, s, md->qkv_out,
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->part, ml,
+                               c.n_heads, c.n_kv_heads, c.max_seq, S);
         RQ_LAUNCH_CHECK();
-        if ((st = launch_gemv_decode_add(L.o, md->attn, md->x, 1, s)) != RQ_OK) return st;
+        if ((st = launch_gemv_decode_attn_add(L.o, md->part, S, c.head_dim, md->x, s)) != RQ_OK) return st;
         if ((st = launch_swiglu_decode_norm(L.gate, L.up, md->x, L.mlp_norm, c.norm_eps, md->h, s)) != RQ_OK)
             return st;
         if ((st = launch_gemv_decode_add(L.down, md->h, md->x, 1, s)) != RQ_OK) return st;
@@ -476,7 +494,12 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     const size_t L = (size_t)c.n_layers, kv = L * (size_t)c.n_kv_heads * c.max_seq * c.head_dim;
     auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
     size_t bytes = L * (pad((size_t)QKV * H) + pad((size_t)QKV * 4));
-    bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(QW * 2) + pad(2 * I * 2) +
+    // attention splits: ~160 positions of the cache per block (each block's K/V
+    // rows stream through one CU), at most 4 (the o-projection re-reads the
+    // partials in every block)
+    const int n_split = c.max_seq <= 160 ? 1 : (c.max_seq <= 320 ? 2 : 4);
+    const size_t part_floats = (size_t)c.n_heads * n_split * (c.head_dim + 2);
+    bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(part_floats * 4) + pad(2 * I * 2) +
              2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4) +
              pad((size_t)c.max_seq * (c.head_dim / 2) * sizeof(float2));
     hipError_t e = hipMalloc(&md->owned, bytes);
@@ -516,7 +539,8 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     md->x = carve<float>(p, H);
     md->qkv_out = carve<float>(p, QKV);
     md->logits = carve<float>(p, c.vocab);
-    md->attn = carve<_Float16>(p, QW);
+    md->part = carve<float>(p, part_floats);
+    md->n_split = n_split;
     md->h = carve<_Float16>(p, 2 * I);
     md->kc = carve<_Float16>(p, kv);
     md->vc = carve<_Float16>(p, kv);
