@@ -319,19 +319,26 @@ int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64
 // serves; the caller then uses the generic kernel.
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 hipStream_t s) {
-    (void)num_cus;
     const int64_t N = w.n_out, K = w.k_in;
     // 32-bit buffer offsets: a 256-row panel of X (256 * K * 2 bytes) must stay below 2^31.
     if (w.format != RQ_Q_ROWWISE_I8 || xt != RQ_F16 || K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) ||
         !aligned(x, 16) || m > 0x7fffffff || N > 0x7fffffff)
         return RQ_ERR_UNSUPPORTED;
     if (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)) return RQ_ERR_UNSUPPORTED;
-    // Measured at M = 2048 (N, K in {4096, 11008}): the 4-stage ring with
-    // groups of 4 token panels per XCD beats the 3-stage / token-major order
-    // by 5-15%; ping-pong fragments beat single-buffered ones at 128x128 too.
-    if (m <= 64) return launch_tiled<64, 128, false, 3, 4>(w, x, y, yt, m, 1, s);
-    if (m < 1024) return launch_tiled<128, 128, true, 4, 4>(w, x, y, yt, m, 4, s);
-    return launch_tiled<256, 128, true, 4, 8>(w, x, y, yt, m, 4, s);
+    // The largest tile whose grid still has >= 2/3 as many tiles as the device
+    // has CUs: a block streams its X and W panels through one CU at a latency-
+    // bound rate, so a grid that leaves CUs idle loses more than smaller tiles
+    // cost.  Measured (N = K = 4096): m = 256 64x64 19.9 us (128x128: 36.2),
+    // m = 512 128x64 28.1 us (38.4), m = 768 128x128 39.0, m = 1536 256x128
+    // 61.2 us (128x128: 76.3); N = 11008, m = 256: 128x128 39.1 (64x64: 41.1).
+    // Groups of 4 token panels per XCD and the ping-pong fragments beat
+    // token-major order and single buffering by 5-15 % at m = 2048.
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    auto fills = [&](int bm, int bn) { return cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
+    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8>(w, x, y, yt, m, 4, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 4>(w, x, y, yt, m, 4, s);
+    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4>(w, x, y, yt, m, 4, s);
+    return launch_tiled<64, 64, true, 4, 4>(w, x, y, yt, m, 4, s);
 }
 
 }  // namespace rq

@@ -170,7 +170,10 @@ def test_config4_prefill(ctx, engine, n, k):
     _check_prefill(y, x, q, s, f"C4 2048x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 136, 2048), (300, 4096, 64), (129, 129, 128)])
+# tile per shape on a 256-CU device: 64x64 for the first, second and fourth, 128x64 for
+# (300, 4096), 128x128 for (770, 4096), 256x128 on 8 waves for (1500, 4100)
+@pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 136, 2048), (300, 4096, 64), (129, 129, 128),
+                                   (770, 4096, 128), (1500, 4100, 64)])
 def test_gemm_ragged(ctx, engine, m, n, k):
     g = synth.rng(m + n + k)
     q, s = synth.rowwise_weight(g, n, k)
