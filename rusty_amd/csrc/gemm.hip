@@ -6,14 +6,16 @@
 //
 // Design (each choice measured on MI355X):
 //  * Block tile BM tokens x BN features, 64 k per step, NW waves in a
-//    (NW/2) x 2 grid, each wave (BM/(NW/2)) x (BN/2) outputs as 32x32 tiles of
-//    v_mfma_f32_32x32x16_f16 (16x16x32 keeps the MFMA pipe only ~50% busy).
-//    MFMA A = W (32 features x 16 k), B = X^T (16 k x 32 tokens): a lane's
-//    accumulator holds runs of 4 consecutive features of one token (8-byte
-//    fp16 stores).  The 256x128 tile runs 8 waves (two per SIMD, 64x64 each,
-//    251 VGPRs with the accumulators): while one wave of a SIMD waits on its
-//    DMA issue or LDS reads the other issues MFMAs (2048x4096x4096:
-//    80.5 -> 74.6 us against 4 waves of 128x64).
+//    (NW/WGN) x WGN grid, each wave (BM/(NW/WGN)) x (BN/WGN) outputs as 32x32
+//    tiles of v_mfma_f32_32x32x16_f16 (16x16x32 keeps the MFMA pipe only ~50%
+//    busy).  MFMA A = W (32 features x 16 k), B = X^T (16 k x 32 tokens): a
+//    lane's accumulator holds runs of 4 consecutive features of one token
+//    (8-byte fp16 stores).  The 256x128 tile runs 8 waves (two per SIMD):
+//    while one wave of a SIMD waits on its DMA issue or LDS reads the other
+//    issues MFMAs (2048x4096x4096: 80.5 -> 74.6 us against 4 waves of
+//    128x64).  Its waves are 128x32 (a 2x4 grid) rather than 64x64: every
+//    wave expands the int8 W fragments it multiplies, so a wave that covers
+//    fewer features repeats less of that VALU work (-2-4 %).
 //  * Staging is direct-to-LDS DMA (buffer_load_dwordx4 ... lds): each wave
 //    moves 1 KiB units from global memory straight into LDS, so tiles never
 //    pass through VGPRs or ds_write (register staging measured ~10% slower,
@@ -117,12 +119,12 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
     tn = r / gsize;
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm) {
-    constexpr int WGN = 2, WGM = NW / WGN;  // wave grid: WGM along tokens, WGN along features
+    constexpr int WGM = NW / WGN;  // wave grid: WGM along tokens, WGN along features
     constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
     constexpr int XUW = BM * 128 / 1024 / NW, WUW = BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
     static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
@@ -300,13 +302,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN>
 int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
                        (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m,
                        (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm);
     RQ_LAUNCH_CHECK();
@@ -335,10 +337,10 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // token-major order and single buffering by 5-15 % at m = 2048.
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     auto fills = [&](int bm, int bn) { return cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8>(w, x, y, yt, m, 4, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 4>(w, x, y, yt, m, 4, s);
-    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4>(w, x, y, yt, m, 4, s);
-    return launch_tiled<64, 64, true, 4, 4>(w, x, y, yt, m, 4, s);
+    if (fills(256, 128)) return launch_tiled<256, 128, false, 4, 8, 4>(w, x, y, yt, m, 4, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 4, 2>(w, x, y, yt, m, 4, s);
+    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, s);
+    return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, s);
 }
 
 }  // namespace rq
