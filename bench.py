@@ -16,6 +16,7 @@ Printed JSON (one line, stdout):
   cpu_baseline     the reference's per-token path on host cores: k-ascending
                    f32 GEMV on the load-time-dequantized f32 weight (oracle port)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
+  prefill_mid      the same GEMM at M=256 and 512 (4096x4096), not a configs[] shape
   decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2])
   swiglu           configs[2]: the fused SwiGLU MLP (gate+up pass, then down)
                    at the 7B shape, M=1 and M=8, GB/s of its algorithmic bytes
@@ -397,6 +398,9 @@ def main() -> int:
             pf.append(prefill(ctx, engine, n, k, steps=args.prefill_steps))
             log(f"prefill {pf[-1]}")
         result["prefill"] = pf
+        # mid-size m (a short prompt, or a batch of decode streams): not a configs[] shape
+        result["prefill_mid"] = [prefill(ctx, engine, 4096, 4096, m=m, steps=args.prefill_steps) for m in (256, 512)]
+        log(f"prefill (mid-size m) {result['prefill_mid']}")
         sw = [swiglu(ctx, engine, m) for m in (1, 8)]
         for e in sw:
             log(f"swiglu {e}")
