@@ -84,6 +84,21 @@ def test_gemv_shapes(ctx, engine, m, k):
     assert ok, (max_abs, rel)
 
 
+@pytest.mark.parametrize("k", [16, 2064, 8208, 16400, 20480])
+@pytest.mark.parametrize("m", [5, 9, 16])
+def test_gemv_skinny_batch_counts(ctx, engine, m, k):
+    # 5 <= m <= 16 runs 8 waves that each take 64-wide k groups in batches of 8,
+    # two batches in flight: these K give every wave 0..5 batches, and
+    # K % 64 != 0 leaves a part-live last group
+    g = synth.rng(m * 7 + k)
+    n = 37  # ragged last row block
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok, (max_abs, rel)
+
+
 @pytest.mark.parametrize("n,k", [(16391, 2048), (20000, 1024), (16384, 5632)])
 def test_gemv_tall_weights(ctx, engine, n, k):
     # n_out >= 16384 at m = 1 runs 8 rows per row group (an lm_head shape);
