@@ -5,17 +5,22 @@
 // (kernels.wgsl:379-400).  MFMA-bound: 2*M*N*K flops over 1 B/weight + 2 B/act.
 //
 // Design (each choice measured on MI355X):
-//  * Block tile BM tokens x BN features, 64 k per step, NW waves in a
-//    (NW/WGN) x WGN grid, each wave (BM/(NW/WGN)) x (BN/WGN) outputs as 32x32
-//    tiles of v_mfma_f32_32x32x16_f16 (16x16x32 keeps the MFMA pipe only ~50%
-//    busy).  MFMA A = W (32 features x 16 k), B = X^T (16 k x 32 tokens): a
-//    lane's accumulator holds runs of 4 consecutive features of one token
-//    (8-byte fp16 stores).  The 256x128 tile runs 8 waves (two per SIMD):
-//    while one wave of a SIMD waits on its DMA issue or LDS reads the other
-//    issues MFMAs (2048x4096x4096: 80.5 -> 74.6 us against 4 waves of
-//    128x64).  Its waves are 128x32 (a 2x4 grid) rather than 64x64: every
-//    wave expands the int8 W fragments it multiplies, so a wave that covers
-//    fewer features repeats less of that VALU work (-2-4 %).
+//  * Block tile BM tokens x BN features, 64 k per step, NW waves as KG
+//    k-groups of (NW/KG/WGN) x WGN waves; each wave (BM/(NW/KG/WGN)) x
+//    (BN/WGN) outputs as 32x32 tiles of v_mfma_f32_32x32x16_f16 (16x16x32
+//    keeps the MFMA pipe only ~50% busy).  MFMA A = W (32 features x 16 k),
+//    B = X^T (16 k x 32 tokens): a lane's accumulator holds runs of 4
+//    consecutive features of one token (8-byte fp16 stores).  The 256x128
+//    and 128x128 tiles run 8 waves (two per SIMD: while one wave of a SIMD
+//    waits on its DMA issue or LDS reads the other issues MFMAs) as two
+//    k-groups: group g multiplies k16 slices 2g, 2g+1 of every stage, so each
+//    wave covers 128 (or 64) tokens x 64 features with the fragment reads and
+//    int8 expansion of half a stage, and the groups add their partial sums
+//    once through the ring at the end.  Against one group of 128x32 waves
+//    the LDS fragment reads per MFMA fall from 1.1 to 0.63 KiB at the same
+//    expansion work: 2048x4096x11008 178.8 -> 172.6 us, m = 768 and 1024 at
+//    N = K = 4096 (128x128 tile, against 4 waves) 38.3 -> 35.5 us and
+//    42.9 -> 40.6 us; 2048x4096x4096 unchanged.
 //  * Staging is direct-to-LDS DMA (buffer_load_dwordx4 ... lds): each wave
 //    moves 1 KiB units from global memory straight into LDS, so tiles never
 //    pass through VGPRs or ds_write (register staging measured ~10% slower,
@@ -119,13 +124,19 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
     tn = r / gsize;
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm) {
-    constexpr int WGM = NW / WGN;  // wave grid: WGM along tokens, WGN along features
+    // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
+    // of every 64-k stage, so a wave tile covers KG times the outputs for the
+    // same fragment bytes; the groups' partial sums meet in LDS at the end.
+    constexpr int WPG = NW / KG;   // waves per k-group
+    constexpr int K16 = 4 / KG;    // 16-k slices per wave per stage
+    constexpr int WGM = WPG / WGN; // wave grid: WGM along tokens, WGN along features
     constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+    static_assert(KG == 1 || (KG == 2 && FN % 2 == 0), "two k-groups split the finishing work by feature tiles");
     constexpr int XUW = BM * 128 / 1024 / NW, WUW = BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
     static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
     static_assert(S >= 3 && S * (BM * 128 + BN * 64) <= 160 * 1024, "ring does not fit in LDS");
@@ -139,7 +150,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     // the wave index as a uniform (scalar) value: LDS bases and DMA offsets
     // derived from it stay in SGPRs instead of being re-derived every k-step
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t / 64), lane = t % 64;
-    const int wm = wave / WGN, wn = wave % WGN;
+    const int kg = wave / WPG, wq = wave % WPG;
+    const int wm = wq / WGN, wn = wq % WGN;
     const int fr = lane % 32, h = lane / 32;
     const int nk = K / 64;
 
@@ -183,35 +195,36 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 
     // A k-step's fragments: raw int8 W (expanded just before the MFMA) and fp16 X.
     struct Frag {
-        uint2 w[4][FN];
-        half8 x[4][FM];
+        uint2 w[K16][FN];
+        half8 x[K16][FM];
     };
     auto fetch = [&](const Stage<BM, BN> &st, Frag &f) {
 #pragma unroll
-        for (int k16 = 0; k16 < 4; ++k16) {
+        for (int kl = 0; kl < K16; ++kl) {
+            const int k16 = kg * K16 + kl;
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
                 const int r = wn * TN + i * 32 + fr;
-                f.w[k16][i] = *reinterpret_cast<const uint2 *>(st.w + r * 64 + ((k16 ^ ((r >> 2) & 3)) * 16) + h * 8);
+                f.w[kl][i] = *reinterpret_cast<const uint2 *>(st.w + r * 64 + ((k16 ^ ((r >> 2) & 3)) * 16) + h * 8);
             }
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int r = wm * TM + j * 32 + fr, c = 2 * k16 + h;
-                f.x[k16][j] = *reinterpret_cast<const half8 *>(st.x + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+                f.x[kl][j] = *reinterpret_cast<const half8 *>(st.x + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
             }
         }
     };
     auto mma = [&](const Frag &f) {
 #pragma unroll
-        for (int k16 = 0; k16 < 4; ++k16) {
+        for (int kl = 0; kl < K16; ++kl) {
             half8 a[FN];
 #pragma unroll
-            for (int i = 0; i < FN; ++i) a[i] = i8x8_to_half8(f.w[k16][i]);
+            for (int i = 0; i < FN; ++i) a[i] = i8x8_to_half8(f.w[kl][i]);
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], f.x[k16][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], f.x[kl][j], acc[i][j], 0, 0, 0);
         }
     };
     // Wait until this wave's DMA for the step about to be read has landed
@@ -262,10 +275,49 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
     wait_vmcnt<0>();  // no DMA in flight past this point
 
+    if constexpr (KG == 2) {
+        // Group g finishes the feature tiles i with i % 2 == g: it hands its
+        // partial sums of the other tiles to the other group through the
+        // (now idle) ring, lane-contiguous 16-byte pieces, and adds the other
+        // group's partials of its own tiles.
+        constexpr int HF = FN / 2;  // feature tiles per group
+        static_assert(2 * WPG * HF * FM * 16 * 64 * 4 <= S * (int)sizeof(Stage<BM, BN>), "exchange does not fit");
+        float4 *xch = reinterpret_cast<float4 *>(&ring[0]);
+        // slot of (target group, wave position, tile pair (i / 2, j), quad r4), then lane
+        auto slot = [&](int tg, int ih, int j, int r4) { return (((tg * WPG + wq) * HF + ih) * FM + j) * 4 + r4; };
+        __syncthreads();  // every wave is done with the ring
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            if (i % 2 == kg) continue;
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    xch[slot(1 - kg, i / 2, j, r4) * 64 + lane] =
+                        make_float4(acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            if (i % 2 != kg) continue;
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const float4 o = xch[slot(kg, i / 2, j, r4) * 64 + lane];
+                    acc[i][j][4 * r4] += o.x;
+                    acc[i][j][4 * r4 + 1] += o.y;
+                    acc[i][j][4 * r4 + 2] += o.z;
+                    acc[i][j][4 * r4 + 3] += o.w;
+                }
+        }
+    }
+
     // Epilogue: acc[i][j][r] = D[feature 8*(r/4) + 4*(lane/32) + r%4][token lane%32]
     // of tile (features n0 + wn*TN + 32 i, tokens m0 + wm*TM + 32 j).
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
+        if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;
@@ -302,13 +354,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
 int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
                        (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m,
                        (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm);
     RQ_LAUNCH_CHECK();
@@ -334,11 +386,13 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // m = 512 128x64 28.1 us (38.4), m = 768 128x128 39.0, m = 1536 256x128
     // 61.2 us (128x128: 76.3); N = 11008, m = 256: 128x128 39.1 (64x64: 41.1).
     // Groups of 4 token panels per XCD and the ping-pong fragments beat
-    // token-major order and single buffering by 5-15 % at m = 2048.
+    // token-major order and single buffering by 5-15 % at m = 2048.  The two
+    // large tiles run two k-groups of 4 waves; at 128x64 and 64x64 one group
+    // of 4 waves measured 2-4 % faster.
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     auto fills = [&](int bm, int bn) { return cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (fills(256, 128)) return launch_tiled<256, 128, false, 4, 8, 4>(w, x, y, yt, m, 4, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 4, 2>(w, x, y, yt, m, 4, s);
+    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, s);
     if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, s);
     return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, s);
 }

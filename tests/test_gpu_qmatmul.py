@@ -87,9 +87,9 @@ def test_gemv_shapes(ctx, engine, m, k):
 @pytest.mark.parametrize("k", [16, 2064, 8208, 16400, 20480])
 @pytest.mark.parametrize("m", [5, 9, 16])
 def test_gemv_skinny_batch_counts(ctx, engine, m, k):
-    # 5 <= m <= 16 runs 8 waves that each take 64-wide k groups in batches of 8,
-    # two batches in flight: these K give every wave 0..5 batches, and
-    # K % 64 != 0 leaves a part-live last group
+    # 5 <= m <= 16 runs 8 (K <= 4096) or 4 waves that each take 64-wide k groups
+    # in batches of 4, two batches in flight: these K give a wave from no batch
+    # to 20 (odd and even counts), and K % 64 != 0 leaves a part-live last group
     g = synth.rng(m * 7 + k)
     n = 37  # ragged last row block
     q, s = synth.rowwise_weight(g, n, k)
@@ -186,9 +186,10 @@ def test_config4_prefill(ctx, engine, n, k):
 
 
 # tile per shape on a 256-CU device: 64x64 for the first, second and fourth, 128x64 for
-# (300, 4096), 128x128 for (770, 4096), 256x128 on 8 waves for (1500, 4100)
+# (300, 4096), 128x128 (two k-groups of 4 waves) for (770, 4096) and (1100, 4100), 256x128
+# (two k-groups) for (1500, 4100); k = 1088 is 17 k-steps, not a multiple of the LDS ring period
 @pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 136, 2048), (300, 4096, 64), (129, 129, 128),
-                                   (770, 4096, 128), (1500, 4100, 64)])
+                                   (770, 4096, 128), (1500, 4100, 64), (1100, 4100, 1088), (1500, 4100, 1088)])
 def test_gemm_ragged(ctx, engine, m, n, k):
     g = synth.rng(m + n + k)
     q, s = synth.rowwise_weight(g, n, k)
