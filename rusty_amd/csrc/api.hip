@@ -278,9 +278,14 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                             int64_t m, hipStream_t s) {
     if (w.k_in > 0) {
+        // 1-2 tokens: the VALU dot2 GEMV; 3-16: the MFMA GEMV (measured faster
+        // from 3 tokens on, e.g. 4096x4096 m = 4: 7.2 -> 6.3 us); the VALU
+        // kernel also serves the 3-4 token shapes the MFMA kernel refuses
+        // (affine codes).
         int st = RQ_ERR_UNSUPPORTED;
-        if (m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
+        if (m <= 2 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 16 && xt == RQ_F16) st = launch_gemv_mfma(w, x, y, yt, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(w, x, xt, y, yt, (int)m, ctx->num_cus, s);
         if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, s);
         if (st != RQ_ERR_UNSUPPORTED) return st;
@@ -325,8 +330,9 @@ int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, con
     hipStream_t s = pick(ctx, stream);
     // gate/up pass -> h (fp16, [m, I])
     st = RQ_ERR_UNSUPPORTED;
-    if (x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
+    if (x_dtype == RQ_F16 && m <= 2) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 16) st = launch_swiglu_mfma(*gate, *up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m > 16) {
         // prefill: gate and up through the GEMM into the two halves of the
         // workspace, then h = silu(g) * u in place over the first half

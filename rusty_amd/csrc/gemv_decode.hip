@@ -1,4 +1,6 @@
 // Decode dequant-GEMV, fp16 activations, m <= 4:  Y[m, n] = sum_k X[m, k] * deq(W)[n, k].
+// Serves m = 1-2, and m = 3-4 for the weights the MFMA GEMV does not take
+// (affine codes); per-row codes at m >= 3 go to the MFMA GEMV.
 //
 // HBM-bound: every weight byte is read once, 16.8 MB for a 4096x4096 layer,
 // a few microseconds per call.  At that size the fixed costs of a launch (wave

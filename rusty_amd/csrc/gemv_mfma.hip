@@ -1,37 +1,33 @@
-// Decode dequant-GEMV on the matrix cores, 5 <= m <= 16 tokens:
+// Decode dequant-GEMV on the matrix cores, 3 <= m <= 16 tokens:
 // Y[m, n] = s[n] * sum_k X[m, k] * q[n, k].
 //
-// Still HBM-bound (every weight byte read once) but with 5-16 activation rows
-// the per-byte arithmetic no longer fits the VALU budget of the dot2 kernel,
+// Still HBM-bound (every weight byte read once) but with 3-16 activation rows
+// the per-byte arithmetic no longer fits the VALU budget of the dot2 kernel
+// (m = 4, 4096x4096: 7.2 us there, 6.3 us here; m = 2 stays faster there),
 // so the products go to v_mfma_f32_16x16x32_f16 (16 features x 16 tokens x 32
 // k per instruction; MFMA throughput is far from the limit here):
 //  * One block of NWV waves per 16 weight rows (SwiGLU: 8 gate + the same 8
-//    up rows).  Wave w takes the 64-k groups w, w + NWV, ...  Per group a lane
-//    (fr = lane % 16, q = lane / 16) loads 16 bytes of weight row fr and 32
-//    bytes (16 fp16) of token fr at k = 64 g + 16 q straight into registers:
-//    they are the operands of two MFMAs, MFMA e covering k = 64 g + 16 q +
-//    8 e + (0..7) in lane group q -- every k of the group once, in the order
-//    the MFMA's k slots take them, for both operands.  No LDS staging: the
-//    activation rows (2 B per element per token) outweigh the weight rows, so
-//    staging both per k-step overflowed LDS before the ring was deep enough.
-//  * All loads of a batch of 4 groups are issued before the first is used
-//    (a scheduling barrier keeps the compiler from interleaving them with
-//    the conversions), and the next batch's loads are in flight while the
-//    current batch is multiplied.  Tokens >= m, rows >= N and k >= K read as
-//    zero.
+//    up rows).  Wave w takes the 256-k batches w, w + NWV, ...
+//  * Weights are loaded as 4 rows x 256 contiguous bytes per instruction
+//    (lane chunk lane % 16 of row 4 i + lane / 16): against loading the MFMA
+//    operand layout directly (16 rows x 64 B per instruction) the weight
+//    streams 15-23 % faster.  Each wave then transposes its batch through its
+//    own 4 KiB of LDS (ds_write_b128, then ds_read_b64 in operand layout, the
+//    16-byte chunks XOR-swizzled by row) -- no barrier, the slice is private.
+//  * Activations go straight from global memory into the B operand: lane
+//    (fr = lane % 16, q = lane / 16) of MFMA j loads 16 bytes of token fr at
+//    k = 256 b + 32 j + 8 q, the k its weight operand holds.
+//  * All loads of a batch are issued before the first is used (a scheduling
+//    barrier keeps the compiler from interleaving them with the conversions),
+//    and the next batch's loads are in flight while the current batch is
+//    multiplied.  Tokens >= m, rows >= N and k >= K read as zero.
 //  * NWV = 8 where the grid is at most two blocks per CU and K <= 4096 (one
 //    block per CU needs the eight waves' loads in flight), else NWV = 4: more
 //    resident blocks per CU did better at K = 11008 or N = 11008.
 //  * The weight is expanded exactly in registers: XOR 0x80, v_perm_b32 under
 //    exponent 0x64 (fp16 1152+q), v_pk_add_f16 -1152.
-//  * The eight waves' 16x16 partial sums meet in LDS once; scale, fp16/f32
-//    store (SwiGLU: h = silu(g) * u).
-// Measured against an LDS-ring version (4 waves, DMA staging, 3 steps in
-// flight per wave), m = 8: 4096x4096 9.3 -> 7.2 us, 11008x4096 22.7 -> 15.7
-// us, 4096x11008 16.5 -> 16.1 us.  Every variant tried (batch 2-8, 4-16
-// waves, 32 rows per block) stays at 2.0-2.9 TB/s: each load instruction
-// covers 16 rows x 64 B of the weight, and every block re-reads the
-// activations (as many bytes as its weight rows at m = 8).
+//  * The waves' 16x16 partial sums meet in LDS once; scale, fp16/f32 store
+//    (SwiGLU: h = silu(g) * u).
 #include "common.hpp"
 
 #include <type_traits>
@@ -39,7 +35,6 @@
 namespace rq {
 namespace {
 
-constexpr int BATCH = 4;    // 64-k groups per wave per batch
 constexpr uint32_t kOOB = 0x80000000u;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -75,9 +70,11 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint32_t lo, uint32_t hi) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// One batch of a wave's operands: BATCH groups x (weight 16 B, activations 2 x 16 B).
+// One batch of a wave's operands: 256 k of the block's 16 weight rows, as
+// loaded (4 rows x 256 B per instruction), and the activations of the 8 MFMAs
+// that consume them (16 B per lane per MFMA, already in operand layout).
 struct Batch {
-    uint4 w[BATCH], xa[BATCH], xb[BATCH];
+    uint4 w[4], x[8];
 };
 
 // SWI: SwiGLU gate/up pass -- the block's 16 weight rows are 8 gate rows (W)
@@ -89,63 +86,86 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
                                                   int m_act, int N, int K) {
     constexpr int RB = SWI ? 8 : 16;  // output rows per block
     __shared__ floatx4 red[NWV][64];
+    // per wave: the 16 rows x 256 k of the batch being multiplied, rows of
+    // 256 B with 16-byte chunk c of row r stored at chunk c ^ r
+    __shared__ __attribute__((aligned(16))) uint8_t wt[NWV][16 * 256];
 
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);  // scalar: the batch loop branches uniformly
     const int fr = lane % 16, q = lane / 16;  // MFMA operand row (weight row / token) and lane group
     const int n0 = blockIdx.x * RB;
     const int rows_here = min(RB, N - n0);
-    const int wrow = SWI ? fr % 8 : fr;  // SwiGLU: lanes 8..15 of a group hold the up rows
-    const bool up = SWI && fr >= 8;
-    const auto rw = make_rsrc((up ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
+    const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
+    const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
-    const uint32_t wbase = (uint32_t)wrow * (uint32_t)K, xbase = (uint32_t)fr * (uint32_t)K * 2u;
-    const bool wrow_ok = wrow < rows_here;
-    const int ng = (K + 63) / 64;
-    constexpr int STEP = NWV * BATCH;  // groups between a wave's consecutive batches
+    // Weight loads: instruction i covers rows 4 i + q, 256 contiguous bytes
+    // each (lane chunk fr); SwiGLU: instructions 0-1 the gate rows 0-7, 2-3
+    // the up rows 0-7.  A row past the weight, or k past K (which would fall
+    // into the next row), reads as zero.
+    const uint32_t xbase = ((uint32_t)fr * (uint32_t)K + 8u * (uint32_t)q) * 2u;
+    uint8_t *wl = wt[wave];
+    const int nb = (K + 255) / 256;  // 256-k batches; wave w takes batches w, w + NWV, ...
 
-    auto load = [&](Batch &b, int g0) {
+    auto load = [&](Batch &b, int bi) {
+        const uint32_t k0 = (uint32_t)bi * 256u;
+        const bool klive = k0 + 16u * (uint32_t)fr < (uint32_t)K;  // K % 16 == 0
 #pragma unroll
-        for (int i = 0; i < BATCH; ++i) {
-            const int k = (g0 + NWV * i) * 64 + 16 * q;
-            const bool live = k < K;  // K % 16 == 0: a live 16-byte piece lies inside the row
-            b.w[i] = bload<2>(rw, live && wrow_ok ? wbase + (uint32_t)k : kOOB);
-            b.xa[i] = bload<0>(rx, live ? xbase + (uint32_t)k * 2u : kOOB);
-            b.xb[i] = bload<0>(rx, live ? xbase + (uint32_t)k * 2u + 16u : kOOB);
+        for (int i = 0; i < 4; ++i) {
+            const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the weight block
+            const bool live = klive && r < rows_here;
+            const uint32_t off = (uint32_t)r * (uint32_t)K + k0 + 16u * (uint32_t)fr;
+            b.w[i] = bload<2>(SWI && i >= 2 ? rw2 : rw, live ? off : kOOB);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t k = k0 + 32u * (uint32_t)j;  // lane k = k + 8 q .. + 8
+            b.x[j] = bload<0>(rx, k + 8u * (uint32_t)q < (uint32_t)K ? xbase + k * 2u : kOOB);
         }
     };
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Transpose through the wave's LDS slice: lane (fr, q) of MFMA j takes the
+    // 8 codes of row fr at k = 32 j + 8 q, the k order of its activations.
+    // Only this wave touches the slice, and LDS operations of a wave complete
+    // in order, so no barrier is needed around it.
     auto mma = [&](const Batch &b) {
 #pragma unroll
-        for (int i = 0; i < BATCH; ++i) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(b.w[i].x, b.w[i].y),
-                                                         __builtin_bit_cast(half8, b.xa[i]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(b.w[i].z, b.w[i].w),
-                                                         __builtin_bit_cast(half8, b.xb[i]), acc, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * i + q;
+            *reinterpret_cast<uint4 *>(wl + r * 256 + ((fr ^ r) << 4)) = b.w[i];
         }
+        uint2 a[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = 2 * j + (q >> 1);
+            a[j] = *reinterpret_cast<const uint2 *>(wl + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(a[j].x, a[j].y),
+                                                         __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
     };
 
     // Two batches alternate: the next one's loads are in flight while the
     // current one is multiplied.  Software-pipelined with a peeled tail so
     // that every load sits in the same straight-line block as the MFMAs that
     // consume it (a load whose only use lies behind a branch gets sunk past
-    // the branch, and the prefetch is lost).  nb, the wave's batch count, is
+    // the branch, and the prefetch is lost).  mb, the wave's batch count, is
     // wave-uniform.
-    const int nb = (ng - wave + STEP - 1) / STEP;
+    const int mb = (nb - wave + NWV - 1) / NWV;
     Batch A, B;
-    if (nb > 0) {
+    if (mb > 0) {
         load(A, wave);
         int b = 0;
-        for (; b + 2 < nb; b += 2) {
-            load(B, wave + (b + 1) * STEP);
+        for (; b + 2 < mb; b += 2) {
+            load(B, wave + (b + 1) * NWV);
             __builtin_amdgcn_sched_barrier(0);  // issue every load before the conversions
             mma(A);
-            load(A, wave + (b + 2) * STEP);
+            load(A, wave + (b + 2) * NWV);
             __builtin_amdgcn_sched_barrier(0);
             mma(B);
         }
-        if (b + 1 < nb) {
-            load(B, wave + (b + 1) * STEP);
+        if (b + 1 < mb) {
+            load(B, wave + (b + 1) * NWV);
             __builtin_amdgcn_sched_barrier(0);
             mma(A);
             mma(B);

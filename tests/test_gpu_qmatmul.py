@@ -85,11 +85,12 @@ def test_gemv_shapes(ctx, engine, m, k):
 
 
 @pytest.mark.parametrize("k", [16, 2064, 8208, 16400, 20480])
-@pytest.mark.parametrize("m", [5, 9, 16])
+@pytest.mark.parametrize("m", [3, 4, 5, 9, 16])
 def test_gemv_skinny_batch_counts(ctx, engine, m, k):
-    # 5 <= m <= 16 runs 8 (K <= 4096) or 4 waves that each take 64-wide k groups
-    # in batches of 4, two batches in flight: these K give a wave from no batch
-    # to 20 (odd and even counts), and K % 64 != 0 leaves a part-live last group
+    # 3 <= m <= 16 runs 8 (K <= 4096) or 4 waves that each take 256-wide k
+    # batches, two in flight: these K give a wave from no batch to 20 (odd and
+    # even counts), and K % 256 != 0 leaves a part-live last batch whose dead
+    # chunks would otherwise read the next row
     g = synth.rng(m * 7 + k)
     n = 37  # ragged last row block
     q, s = synth.rowwise_weight(g, n, k)
