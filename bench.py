@@ -299,6 +299,24 @@ def cpu_baseline(seconds: float):
                        f"bytes counted as the int8 algorithmic bytes of the GPU step")}
 
 
+def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
+    """configs[1] at M = 4, 16 and the SwiGLU-shaped GEMVs at M = 1, 8, each
+    over enough rotating weight copies to stay out of the Infinity Cache."""
+    extra = {}
+    for m, n, k in ((4, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 11008, 4096), (1, 4096, 11008),
+                    (8, 4096, 11008)):
+        copies = max(2, min(COPIES, (600 << 20) // (n * k)))
+        w2 = GemvWorkload(ctx, m, n, k, copies=copies)
+        wms = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
+        kms = wms / (20 * copies)
+        extra[f"m{m}_{n}x{k}"] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1),
+                                  "us_per_launch": round(kms * 1e3, 2),
+                                  "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"GEMV m={m} {n}x{k}: {extra[f'm{m}_{n}x{k}']}")
+        del w2
+    return extra
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -311,7 +329,7 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["prefill", "swiglu", "decode"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps as direct launches instead of one graph per token (for tools that "
@@ -332,7 +350,9 @@ def main() -> int:
 
     if args.only:
         out = {"only": args.only}
-        if args.only == "prefill":
+        if args.only == "gemv":
+            out["decode_gemv"] = decode_gemv_extra(ctx, use_graph=not args.no_graph)
+        elif args.only == "prefill":
             out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph)
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
         elif args.only == "swiglu":
@@ -380,19 +400,7 @@ def main() -> int:
     }
 
     if not args.quick:
-        extra = {}
-        for m, n, k in ((4, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 11008, 4096), (1, 4096, 11008),
-                        (8, 4096, 11008)):
-            copies = max(2, min(COPIES, (600 << 20) // (n * k)))
-            w2 = GemvWorkload(ctx, m, n, k, copies=copies)
-            wms = time_steps(ctx, w2, 20 * copies, 2 * copies)
-            kms = wms / (20 * copies)
-            extra[f"m{m}_{n}x{k}"] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1),
-                                      "us_per_launch": round(kms * 1e3, 2),
-                                      "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-            log(f"GEMV m={m} {n}x{k}: {extra[f'm{m}_{n}x{k}']}")
-            del w2
-        result["decode_gemv"] = extra
+        result["decode_gemv"] = decode_gemv_extra(ctx)
         pf = []
         for n, k in ((4096, 4096), (11008, 4096), (4096, 11008)):
             pf.append(prefill(ctx, engine, n, k, steps=args.prefill_steps))
