@@ -93,7 +93,8 @@ const char *rq_last_error(void);
  * Replaces UnifiedTensor::{new, empty, to_vec} (lib.rs:115-240): device
  * allocation, host->device upload, device->host readback.  Unlike the
  * reference's pooled `empty()` (pool.rs:30-56, stale contents), rq_alloc
- * memory is uninitialised and rq_memset clears it explicitly. */
+ * memory is uninitialised and rq_memset clears it explicitly (with a fill
+ * kernel, not a memset node, so it may be captured in a HIP graph). */
 int rq_alloc(rq_ctx *ctx, size_t bytes, void **dptr);
 int rq_free(rq_ctx *ctx, void *dptr);
 int rq_memcpy_h2d(rq_ctx *ctx, void *dst, const void *src, size_t bytes, rq_stream stream);

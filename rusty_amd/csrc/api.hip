@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 
 #include "common.hpp"
@@ -60,6 +61,21 @@ int rq::check_qweight(const rq_qweight *w) {
 __global__ void k_device_delay(uint64_t ticks) {
     const uint64_t t0 = wall_clock64();
     while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(32);
+}
+
+// Byte fill: 16-byte stores over the aligned middle (grid-stride), single
+// bytes for the unaligned head and tail.  A kernel rather than
+// hipMemsetAsync, so that a caller may capture it in a HIP graph: memset
+// nodes in captured graphs have given wrong results on replays here.
+__global__ __launch_bounds__(256) void k_fill_bytes(uint8_t *__restrict__ dst, uint32_t v4, size_t head, size_t chunks,
+                                                   size_t n) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+    const uint4 v = make_uint4(v4, v4, v4, v4);
+    uint4 *mid = reinterpret_cast<uint4 *>(dst + head);
+    for (size_t i = t; i < chunks; i += stride) mid[i] = v;
+    const size_t tail0 = head + chunks * 16;
+    if (t < head) dst[t] = (uint8_t)v4;
+    if (t < n - tail0) dst[tail0 + t] = (uint8_t)v4;
 }
 
 extern "C" {
@@ -197,7 +213,13 @@ int rq_memset(rq_ctx *ctx, void *dst, int value, size_t bytes, rq_stream stream)
     RQ_ENTER(ctx);
     if (bytes == 0) return RQ_OK;
     if (!dst) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer in memset");
-    RQ_HIP_TRY(hipMemsetAsync(dst, value, bytes, pick(ctx, stream)));
+    const uint32_t b = (uint32_t)(value & 0xff), v4 = b * 0x01010101u;
+    const size_t mis = reinterpret_cast<uintptr_t>(dst) % 16, head = mis ? std::min(bytes, 16 - mis) : 0;
+    const size_t chunks = (bytes - head) / 16;  // the tail (< 16 bytes) is what remains
+    const size_t blocks = std::min<size_t>(std::max<size_t>(cdiv((int64_t)chunks, 256), 1), 4096);
+    hipLaunchKernelGGL(k_fill_bytes, dim3((unsigned)blocks), dim3(256), 0, pick(ctx, stream), static_cast<uint8_t *>(dst),
+                       v4, head, chunks, bytes);
+    RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 

@@ -24,3 +24,39 @@ def test_device_delay_limits(ctx):
     assert lib.rq_device_delay(ctx.handle, 100001, None) == _lib.RQ_ERR_INVALID_ARGUMENT
     assert b"100000" in lib.rq_last_error()
     ctx.sync()
+
+
+# rq_memset: a fill kernel, exact for any alignment and length, and safe to
+# capture in a HIP graph (replayed several times with eager writes between)
+
+@pytest.mark.parametrize("offset,nbytes", [(0, 0), (0, 1), (3, 5), (1, 16), (7, 33), (0, 4096), (5, 100003)])
+def test_memset_bytes(ctx, offset, nbytes):
+    import numpy as np
+
+    from rusty_amd import DType, UnifiedTensor
+
+    total = offset + nbytes + 37
+    buf = UnifiedTensor.new(ctx, np.full(total, 0xAB, np.uint8), dtype=DType.U8)
+    _lib.call("rq_memset", ctx.handle, buf.ptr + offset, 0x5C, nbytes, None)
+    got = buf.to_vec()
+    want = np.full(total, 0xAB, np.uint8)
+    want[offset:offset + nbytes] = 0x5C
+    assert np.array_equal(got, want)
+
+
+def test_memset_in_graph_replays(ctx):
+    import numpy as np
+
+    from rusty_amd import DType, UnifiedTensor
+    from rusty_amd.hiprt import Graph
+
+    n = 1 << 20
+    buf = UnifiedTensor.new(ctx, np.full(n + 9, 7, np.uint8), dtype=DType.U8)
+    g = Graph(ctx.stream, lambda: _lib.call("rq_memset", ctx.handle, buf.ptr + 3, 0, n, None))
+    ones = np.full(n + 9, 0xFF, np.uint8)
+    for _ in range(4):
+        _lib.call("rq_memcpy_h2d", ctx.handle, buf.ptr, ones.ctypes.data, n + 9, None)  # eager write between replays
+        g.launch()
+        ctx.sync()
+        got = buf.to_vec()
+        assert (got[3:3 + n] == 0).all() and (got[:3] == 0xFF).all() and (got[3 + n:] == 0xFF).all()
