@@ -56,10 +56,13 @@ def run_collect(runner, prompt, steps):
                 max_seq=300),
     LlamaConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=256, vocab=300,
                 max_seq=400),
-], ids=["gqa2_hd64", "mqa_hd128", "mha_long", "gqa2_hd128_long"])
+    LlamaConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=256, vocab=300,
+                max_seq=600),
+], ids=["gqa2_hd64", "mqa_hd128", "mha_long", "gqa2_hd128_long", "gqa2_hd128_600"])
 def test_small_models_match_oracle(ctx, cfg):
     # the runner splits each head's attention over 1 (max_seq <= 160), 2 (<= 320) or 4 blocks:
-    # these models cover 1 and 2 at head_dim 64, 1 and 4 at head_dim 128 (the 1.1B test: 4 at 64)
+    # these models cover 1 and 2 at head_dim 64, 1 and 4 at head_dim 128 (the 1.1B test: 4 at 64);
+    # the 600-position model's splits reach 150 positions, more than one 128-row pass at head_dim 128
     w = synth_weights(cfg, seed=cfg.hidden + cfg.vocab)
     g = np.random.default_rng(11)
     n_prompt = min(40, cfg.max_seq // 2) if cfg.max_seq < 200 else 280
