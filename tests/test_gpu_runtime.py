@@ -60,3 +60,57 @@ def test_memset_in_graph_replays(ctx):
         ctx.sync()
         got = buf.to_vec()
         assert (got[3:3 + n] == 0).all() and (got[:3] == 0xFF).all() and (got[3 + n:] == 0xFF).all()
+
+
+# The hot path captured once in a HIP graph and replayed with new activations
+# written (eagerly) between replays: every replay must match the oracle.
+
+@pytest.mark.parametrize("m", [1, 8, 300])
+def test_qmatmul_graph_replays(ctx, engine, m):
+    import numpy as np
+
+    from conftest import f16_tol_check
+    from oracle import oracle as orc
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+    from rusty_amd.hiprt import Graph
+
+    g = synth.rng(900 + m)
+    q, s = synth.rowwise_weight(g, 520, 1024)
+    w = QuantizedTensor.rowwise(ctx, q, s)
+    X = UnifiedTensor.empty(ctx, [m, 1024], DType.FP16)
+    Y = UnifiedTensor.empty(ctx, [m, 520], DType.FP16)
+    graph = Graph(ctx.stream, lambda: engine.qmatmul(ctx, X, w, Y))
+    for rep in range(3):
+        x = synth.activations(g, m, 1024)
+        _lib.call("rq_memcpy_h2d", ctx.handle, X.ptr, x.ctypes.data, x.nbytes, None)
+        graph.launch()
+        ctx.sync()
+        _, _, ok = f16_tol_check(Y.to_vec(), orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+        assert ok, f"replay {rep}"
+
+
+def test_swiglu_graph_replays(ctx, engine):
+    import numpy as np
+
+    from conftest import f16_tol_check
+    from oracle import oracle as orc
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+    from rusty_amd.hiprt import Graph
+
+    g = synth.rng(950)
+    wg, sg = synth.rowwise_weight(g, 384, 512)
+    wu, su = synth.rowwise_weight(g, 384, 512)
+    wd, sd = synth.rowwise_weight(g, 512, 384)
+    G, U, D = (QuantizedTensor.rowwise(ctx, a, b) for a, b in ((wg, sg), (wu, su), (wd, sd)))
+    for m in (1, 4):
+        X = UnifiedTensor.empty(ctx, [m, 512], DType.FP16)
+        Y = UnifiedTensor.empty(ctx, [m, 512], DType.FP32)
+        H = UnifiedTensor.empty(ctx, [2, m, 384], DType.FP16)
+        graph = Graph(ctx.stream, lambda: engine.mlp_swiglu(ctx, X, G, U, D, Y, H))
+        for rep in range(3):
+            x = synth.activations(g, m, 512)
+            _lib.call("rq_memcpy_h2d", ctx.handle, X.ptr, x.ctypes.data, x.nbytes, None)
+            graph.launch()
+            ctx.sync()
+            truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32))
+            assert f16_tol_check(Y.to_vec(), truth)[2], f"m={m} replay {rep}"
