@@ -114,11 +114,28 @@ int rq_ctx_create(int device, rq_ctx **out) {
     if (!ctx) return fail(RQ_ERR_ALLOC, "context allocation failed");
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
+    ctx->sk_partials = nullptr;
+    ctx->sk_counters = nullptr;
     // Default priority on purpose: streams of mixed priorities are not used.
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete ctx;
         return fail(RQ_ERR_HIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
+    }
+    // Split-K workspace of the prefill GEMM (32 MiB of partial sums, 512 KiB
+    // of counters that must start at zero).  Without it the GEMM never splits.
+    {
+        const size_t part = kGemmSkFloats * 4, cnt = (size_t)kGemmSkCounters * 128;
+        void *p = nullptr;
+        if (hipMalloc(&p, part + cnt) == hipSuccess) {
+            if (hipMemset(static_cast<char *>(p) + part, 0, cnt) == hipSuccess && hipDeviceSynchronize() == hipSuccess) {
+                ctx->sk_partials = static_cast<float *>(p);
+                ctx->sk_counters = reinterpret_cast<int *>(static_cast<char *>(p) + part);
+            } else {
+                (void)hipFree(p);
+            }
+        }
+        (void)hipGetLastError();  // a failed optional allocation is not the caller's error
     }
     *out = ctx;
     return RQ_OK;
@@ -129,6 +146,7 @@ int rq_ctx_destroy(rq_ctx *ctx) {
     RQ_ENTER(ctx);
     hipError_t e1 = hipStreamSynchronize(ctx->stream);
     hipError_t e2 = hipStreamDestroy(ctx->stream);
+    if (ctx->sk_partials) (void)hipFree(ctx->sk_partials);
     delete ctx;
     if (e1 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e1));
     if (e2 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamDestroy: %s", hipGetErrorString(e2));
@@ -294,6 +312,11 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 
 }  // extern "C"
 
+rq::GemmWorkspace rq::gemm_workspace(const rq_ctx *ctx, hipStream_t s) {
+    if (!ctx->sk_partials || s != ctx->stream) return GemmWorkspace{nullptr, nullptr, 0, 0};
+    return GemmWorkspace{ctx->sk_partials, ctx->sk_counters, kGemmSkFloats, kGemmSkCounters};
+}
+
 // Fused linear dispatch (arguments already validated): decode kernels for
 // few tokens, the MFMA GEMM for many, the generic kernel for anything the
 // tuned paths do not serve.
@@ -309,7 +332,7 @@ int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dty
         if (st == RQ_ERR_UNSUPPORTED && m <= 16 && xt == RQ_F16) st = launch_gemv_mfma(w, x, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(w, x, xt, y, yt, (int)m, ctx->num_cus, s);
-        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, s);
+        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, gemm_workspace(ctx, s), s);
         if (st != RQ_ERR_UNSUPPORTED) return st;
     }
     return launch_qlinear_generic(w, x, xt, y, yt, m, s);
@@ -359,8 +382,8 @@ int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, con
         // prefill: gate and up through the GEMM into the two halves of the
         // workspace, then h = silu(g) * u in place over the first half
         _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
-        st = launch_gemm(*gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, s);
-        if (st == RQ_OK) st = launch_gemm(*up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, s);
+        st = launch_gemm(*gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, gemm_workspace(ctx, s), s);
+        if (st == RQ_OK) st = launch_gemm(*up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, gemm_workspace(ctx, s), s);
         if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
     }
     if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(*gate, *up, x, x_dtype, h, m, s);

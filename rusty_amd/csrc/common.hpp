@@ -14,6 +14,10 @@ struct rq_ctx {
     int device;
     hipStream_t stream;
     int num_cus;
+    // Split-K workspace of the prefill GEMM (partial sums and per-tile
+    // arrival counters), allocated at create; null if that allocation failed.
+    float *sk_partials;
+    int *sk_counters;
 };
 
 namespace rq {
@@ -71,8 +75,21 @@ int launch_gemv_decode_norm(const rq_qweight &w, const float *x, const _Float16 
 int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
 int launch_gemv(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m,
                 int num_cus, hipStream_t s);
-int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
-                int num_cus, hipStream_t s);
+// Split-K workspace of the prefill GEMM: kGemmSkFloats f32 partial sums and
+// kGemmSkCounters per-tile counters (one 128-byte line each, zero between launches).
+constexpr size_t kGemmSkFloats = (size_t)8 << 20;  // 32 MiB
+constexpr int kGemmSkCounters = 4096;
+struct GemmWorkspace {
+    float *partials;  // null: no split-K
+    int *counters;
+    size_t floats;
+    int n_counters;
+};
+// The workspace of ctx when work on stream s may use it: the context's own
+// stream only (two GEMMs running at once on different streams would share it).
+GemmWorkspace gemm_workspace(const rq_ctx *ctx, hipStream_t s);
+int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
+                const GemmWorkspace &ws, hipStream_t s);
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                            int64_t m, hipStream_t s);
 int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);

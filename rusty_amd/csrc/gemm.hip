@@ -42,6 +42,7 @@
 //  * XCD-aware tile order (tile_of): the blocks one XCD runs together cover a
 //    group of GM token panels x the matching feature panels, so their X and
 //    W panels are shared in that XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -55,6 +56,11 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Split-K workspace layout: partial sums per (tile, split) slot of BM x BN f32;
+// one arrival counter per tile on its own 128-byte line.
+constexpr int kSkCounterStride = 32;
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -115,7 +121,7 @@ struct Stage {
 // group).  The 32 concurrent tiles of one XCD then cover GM token panels x
 // 32/GM feature panels, so both X and W panels are reused in that XCD's L2.
 __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm, int &tm, int &tn) {
-    const int tiles = tiles_m * tiles_n;
+    const int tiles = tiles_m * tiles_n;  // b < tiles
     const int L = (tiles % 8 == 0) ? (b % 8) * (tiles / 8) + b / 8 : b;
     const int per_group = gm * tiles_n;
     const int first_m = (L / per_group) * gm;
@@ -129,7 +135,8 @@ template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
-                                                     int gm) {
+                                                     int gm, int splits, float *__restrict__ skw,
+                                                     int *__restrict__ skc) {
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -145,8 +152,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 
     __shared__ __attribute__((aligned(1024))) Stage<BM, BN> ring[S];
 
+    // Split-K (splits > 1): block b multiplies tile b % tiles over the split
+    // b / tiles of its k-steps; the tile's last block to finish adds every
+    // split's partial sums (see below).
+    const int tiles = tiles_m * tiles_n, tile = blockIdx.x % tiles, split = blockIdx.x / tiles;
     int tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, gm, tm, tn);
+    tile_of(tile, tiles_m, tiles_n, gm, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     // the wave index as a uniform (scalar) value: LDS bases and DMA offsets
     // derived from it stay in SGPRs instead of being re-derived every k-step
@@ -154,7 +165,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     const int kg = wave / WPG, wq = wave % WPG;
     const int wm = wq / WGN, wn = wq % WGN;
     const int fr = lane % 32, h = lane / 32;
-    const int nk = K / 64;
+    const int nk_all = K / 64, ks = (nk_all + splits - 1) / splits;
+    const int k0 = split * ks, nk = min(ks, nk_all - k0);  // this block's k-steps [k0, k0 + nk)
 
     const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
     const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
@@ -178,6 +190,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_void *)&ring[0];
     auto dma = [&](int stage, int kt) {
         const bool live = kt < nk;
+        kt += k0;
         const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)sizeof(Stage<BM, BN>);
         const uint32_t sw = sx + (uint32_t)(BM * 128);  // the W tile follows the X tile
 #pragma unroll
@@ -325,6 +338,73 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         }
     }
 
+    // Split-K: the tiles this wave finishes go to slot (tile, split) of the
+    // workspace as lane-contiguous float4 pieces, stored and later read with
+    // sc1 (device-coherent: the blocks of a tile may sit on different XCDs,
+    // whose L2s are not coherent with each other).  Once its pieces have
+    // landed, a block counts itself on the tile's counter; the block that
+    // arrives last clears the counter for the next launch and adds all the
+    // splits' partials in split order (deterministic whichever block is last)
+    // before the epilogue.  No block waits for another.
+    if constexpr (BM == 64 && BN == 64) {  // larger tiles are chosen only for grids that fill the device
+        if (splits > 1) {
+            constexpr int FNO = FN / KG;  // feature tiles this wave finishes
+            const size_t slot_floats = (size_t)BM * BN;
+            auto piece = [&](int i, int jj, int r4) {
+                return ((((wave * FNO + i / KG) * FM + jj) * 4 + r4) * 64 + lane) * 16u;
+            };
+            {
+                const auto rs = make_rsrc(skw + ((size_t)tile * splits + split) * slot_floats, (uint32_t)slot_floats * 4u);
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    if (KG == 2 && i % 2 != kg) continue;
+#pragma unroll
+                    for (int jj = 0; jj < FM; ++jj)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            // whole vectors: a bit_cast of an ext-vector element reads element 0
+                            const floatx4 v = {acc[i][jj][4 * r4], acc[i][jj][4 * r4 + 1], acc[i][jj][4 * r4 + 2],
+                                               acc[i][jj][4 * r4 + 3]};
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, piece(i, jj, r4),
+                                                                   0, 16);
+                        }
+                }
+            }
+            wait_vmcnt<0>();  // this thread's pieces have landed
+            __shared__ int last;
+            __syncthreads();  // ... and every thread's
+            if (t == 0)
+                last = __hip_atomic_fetch_add(&skc[tile * kSkCounterStride], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+            __syncthreads();
+            if (!last) return;
+            if (t == 0) __hip_atomic_store(&skc[tile * kSkCounterStride], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FM; ++jj)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
+#pragma unroll 1
+            for (int sp = 0; sp < splits; ++sp) {
+                const auto rs = make_rsrc(skw + ((size_t)tile * splits + sp) * slot_floats, (uint32_t)slot_floats * 4u);
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    if (KG == 2 && i % 2 != kg) continue;
+#pragma unroll
+                    for (int jj = 0; jj < FM; ++jj)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            const floatx4 v = __builtin_bit_cast(
+                                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, piece(i, jj, r4), 0, 16));
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][jj][4 * r4 + e] += v[e];
+                        }
+                }
+            }
+        }
+    }
+
     // Epilogue: acc[i][j][r] = D[feature 8*(r/4) + 4*(lane/32) + r%4][token lane%32]
     // of tile (features n0 + wn*TN + 32 i, tokens m0 + wm*TM + 32 j).
     // Staged through the (idle) ring: the scaled tile goes to LDS row by row,
@@ -423,15 +503,32 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
 }
 
+// Split-K when the tile grid covers at most half the CUs (few tokens: each
+// block would otherwise walk all K alone, at a latency-bound rate per
+// k-step): as many splits as keep one block per CU, at least 8 k-steps each,
+// within the context's workspace.  Blocks sharing a CU gained nothing
+// (64x11008x4096, 172 tiles: 23.7 us unsplit, 31-37 us at 2-8 splits), while
+// 64x4096x4096 (64 tiles) went 18.8 -> 10.3 us at 4 splits.  Only on the
+// context's own stream (ws.partials is null otherwise), and only the 64x64
+// tile (the larger ones are chosen only for grids that fill the device).
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
-int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, hipStream_t s) {
+int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, int64_t cus,
+                 const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG>), dim3((unsigned)tiles), dim3(64 * NW), 0, s,
-                       (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m,
-                       (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm);
+    const int64_t nk = K / 64;
+    int64_t splits = 1;
+    if (BM == 64 && BN == 64 && ws.partials && nk >= 16 && 2 * tiles <= cus && tiles <= ws.n_counters) {
+        splits = std::min<int64_t>(nk / 8, cus / tiles);
+        while (splits > 1 && (size_t)(tiles * splits) * BM * BN > ws.floats) --splits;
+        splits = cdiv(nk, cdiv(nk, splits));  // every split gets k-steps (the kernel's ks = ceil(nk / splits))
+    }
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG>), dim3((unsigned)(tiles * splits)),
+                       dim3(64 * NW), 0, s, (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y,
+                       yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm, (int)splits,
+                       ws.partials, ws.counters);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
@@ -441,7 +538,7 @@ int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64
 // Returns RQ_ERR_UNSUPPORTED (without launching) outside what k_gemm_rowwise
 // serves; the caller then uses the generic kernel.
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
-                hipStream_t s) {
+                const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     // 32-bit buffer offsets: a 256-row panel of X (256 * K * 2 bytes) must stay below 2^31.
     if (w.format != RQ_Q_ROWWISE_I8 || xt != RQ_F16 || K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) ||
@@ -460,10 +557,10 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // of 4 waves measured 2-4 % faster.
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     auto fills = [&](int bm, int bn) { return cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, s);
-    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, s);
-    return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, s);
+    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
+    return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
 }
 
 }  // namespace rq

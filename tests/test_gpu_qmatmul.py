@@ -200,6 +200,26 @@ def test_gemm_ragged(ctx, engine, m, n, k):
     assert ok, (max_abs, rel)
 
 
+# Split-K (tile grids covering at most half of a 256-CU device): 17 and 64 tokens at 4096x4096
+# (64 tiles of 64x64, 4 splits of 16 k-steps), 30 tokens at 1000x11008 (16 tiles, 16 splits of
+# 11 k-steps, the last of 7), 100 tokens at 1000x1088 (32 tiles; 17 k-steps allow 2 splits of at
+# least 8: 9 and 8).  The last block
+# of a tile adds the splits in order, so a repeated call must agree bit for bit; f32 output included.
+@pytest.mark.parametrize("m,n,k,ydt", [(17, 4096, 4096, np.float16), (64, 4096, 4096, np.float32),
+                                       (30, 1000, 11008, np.float16), (100, 1000, 1088, np.float16)])
+def test_gemm_split_k(ctx, engine, m, n, k, ydt):
+    g = synth.rng(m + n + k + 3)
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, m, k, sigma=0.5)
+    w = QuantizedTensor.rowwise(ctx, q, s)
+    y = qmm(ctx, engine, w, x, ydt)
+    assert np.isfinite(y).all()
+    assert np.array_equal(y.view(np.uint8), qmm(ctx, engine, w, x, ydt).view(np.uint8)), "repeat differs"
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    report(f"split-K {m}x{n}x{k}", max_abs, rel)
+    assert ok
+
+
 # ---- generic path, edge cases, errors -------------------------------------------
 
 @pytest.mark.parametrize("m,n,k,fmt", [(1, 50, 1000, 0), (3, 7, 33, 0), (20, 31, 100, 0), (2, 40, 96, 1),
