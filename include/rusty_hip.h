@@ -68,8 +68,9 @@ typedef void *rq_stream; /* a hipStream_t; NULL selects the context stream */
 /* ---- context ------------------------------------------------------------
  * Replaces WgpuContext::new (rusty-backend/src/lib.rs:20-47) +
  * ComputeEngine::new (lib.rs:343-4017): selects the device, creates the
- * context's stream (default priority).  Fails with RQ_ERR_NO_DEVICE unless
- * the device is a gfx950. */
+ * context's stream (default priority) and a 32.5 MB workspace the prefill
+ * GEMM uses for split-K partial sums (if that allocation fails the GEMM just
+ * never splits).  Fails with RQ_ERR_NO_DEVICE unless the device is a gfx950. */
 int rq_ctx_create(int device, rq_ctx **out);
 int rq_ctx_destroy(rq_ctx *ctx);
 int rq_ctx_stream(rq_ctx *ctx, rq_stream *out);
@@ -156,7 +157,11 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * forward (Linear::forward, rusty-graph/src/lib.rs:69-70 ->
  * Tensor::matmul, rusty-autograd/src/lib.rs:468-477).
  * x_dtype/y_dtype: RQ_F16 or RQ_F32; accumulation is f32.
- * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM. */
+ * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM.  On the
+ * context's own stream (stream NULL) a GEMM with few tokens splits K over
+ * more blocks using the context's workspace, so two such calls of one
+ * context must not run concurrently (they cannot on one stream); on any
+ * other stream it does not split. */
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y,
                rq_dtype y_dtype, int64_t m, rq_stream stream);
 
