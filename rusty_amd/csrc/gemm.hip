@@ -346,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     // arrives last clears the counter for the next launch and adds all the
     // splits' partials in split order (deterministic whichever block is last)
     // before the epilogue.  No block waits for another.
-    if constexpr (BM == 64 && BN == 64) {  // larger tiles are chosen only for grids that fill the device
+    if constexpr (BM == 64 && BN == 64) {  // only the 64x64 grids split (see launch_tiled)
         if (splits > 1) {
             constexpr int FNO = FN / KG;  // feature tiles this wave finishes
             const size_t slot_floats = (size_t)BM * BN;
@@ -385,21 +385,44 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
                 for (int jj = 0; jj < FM; ++jj)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
+            // UNR splits per round trip (their pieces loaded together, ~64
+            // VGPRs), added in split order
+            constexpr int PIECES = FNO * FM * 4, UNR = PIECES >= 16 ? 1 : 16 / PIECES;
+            auto rsrc_of = [&](int sp) {
+                return make_rsrc(skw + ((size_t)tile * splits + sp) * slot_floats, (uint32_t)slot_floats * 4u);
+            };
 #pragma unroll 1
-            for (int sp = 0; sp < splits; ++sp) {
-                const auto rs = make_rsrc(skw + ((size_t)tile * splits + sp) * slot_floats, (uint32_t)slot_floats * 4u);
+            for (int sp0 = 0; sp0 < splits; sp0 += UNR) {
+                floatx4 v[UNR][PIECES];
 #pragma unroll
-                for (int i = 0; i < FN; ++i) {
-                    if (KG == 2 && i % 2 != kg) continue;
+                for (int u = 0; u < UNR; ++u) {
+                    const auto rs = rsrc_of(min(sp0 + u, splits - 1));
+                    int p = 0;
 #pragma unroll
-                    for (int jj = 0; jj < FM; ++jj)
+                    for (int i = 0; i < FN; ++i) {
+                        if (KG == 2 && i % 2 != kg) continue;
 #pragma unroll
-                        for (int r4 = 0; r4 < 4; ++r4) {
-                            const floatx4 v = __builtin_bit_cast(
-                                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, piece(i, jj, r4), 0, 16));
+                        for (int jj = 0; jj < FM; ++jj)
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[i][jj][4 * r4 + e] += v[e];
-                        }
+                            for (int r4 = 0; r4 < 4; ++r4, ++p)
+                                v[u][p] = __builtin_bit_cast(
+                                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, piece(i, jj, r4), 0, 16));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) {
+                    if (sp0 + u >= splits) break;
+                    int p = 0;
+#pragma unroll
+                    for (int i = 0; i < FN; ++i) {
+                        if (KG == 2 && i % 2 != kg) continue;
+#pragma unroll
+                        for (int jj = 0; jj < FM; ++jj)
+#pragma unroll
+                            for (int r4 = 0; r4 < 4; ++r4, ++p)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[i][jj][4 * r4 + e] += v[u][p][e];
+                    }
                 }
             }
         }
@@ -503,14 +526,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
 }
 
-// Split-K when the tile grid covers at most half the CUs (few tokens: each
-// block would otherwise walk all K alone, at a latency-bound rate per
-// k-step): as many splits as keep one block per CU, at least 8 k-steps each,
-// within the context's workspace.  Blocks sharing a CU gained nothing
-// (64x11008x4096, 172 tiles: 23.7 us unsplit, 31-37 us at 2-8 splits), while
-// 64x4096x4096 (64 tiles) went 18.8 -> 10.3 us at 4 splits.  Only on the
-// context's own stream (ws.partials is null otherwise), and only the 64x64
-// tile (the larger ones are chosen only for grids that fill the device).
+// Split-K for 64x64 tile grids that leave CUs idle (few tokens: each block
+// would otherwise walk all K alone, at a latency-bound rate per k-step): up
+// to half the CUs, as many splits as keep one block per CU; up to 3/4, two
+// splits (the 64x64 kernel fits three blocks per CU); at least 8 k-steps per
+// split, within the context's workspace.  Measured at 4096x4096: 64 tiles
+// 18.8 -> 10.3 us (4 splits; 8: 11.6), 128 tiles 18.6 -> 13.2 (2 splits),
+// 192 tiles 18.6 -> 17.5 (2), 256 tiles best unsplit; 172 tiles at
+// N = 11008: 19.0 -> 17.7 (2).  Only on the context's own stream (ws.partials
+// is null otherwise); the larger tiles gained nothing from splitting (their
+// LDS rings allow one block per CU).
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
 int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, int64_t cus,
                  const GemmWorkspace &ws, hipStream_t s) {
@@ -520,8 +545,8 @@ int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
     const int64_t nk = K / 64;
     int64_t splits = 1;
-    if (BM == 64 && BN == 64 && ws.partials && nk >= 16 && 2 * tiles <= cus && tiles <= ws.n_counters) {
-        splits = std::min<int64_t>(nk / 8, cus / tiles);
+    if (BM == 64 && BN == 64 && ws.partials && nk >= 16 && 4 * tiles <= 3 * cus && tiles <= ws.n_counters) {
+        splits = std::min<int64_t>(nk / 8, 2 * tiles <= cus ? cus / tiles : 2);
         while (splits > 1 && (size_t)(tiles * splits) * BM * BN > ws.floats) --splits;
         splits = cdiv(nk, cdiv(nk, splits));  // every split gets k-steps (the kernel's ks = ceil(nk / splits))
     }
@@ -556,7 +581,9 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // large tiles run two k-groups of 4 waves; at 128x64 and 64x64 one group
     // of 4 waves measured 2-4 % faster.
     const int64_t cus = num_cus > 0 ? num_cus : 256;
-    auto fills = [&](int bm, int bn) { return cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
+    // a tile taller than the tokens (rounded up to 64) only multiplies padding:
+    // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
+    auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
     if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
     if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
     if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
