@@ -64,15 +64,36 @@ constexpr int kMaxSeq = 32768;  // KV cache capacity limit (32-bit cache offsets
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane steps as DPP operand modifiers (one VALU op each) instead of
+// LDS-routed shuffles; whole-wave results through four readlanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// Sum over aligned groups of G lanes (G = 8 or 16); every lane of a group
+// receives its group's sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 8 || G == 16, "DPP row steps cover groups of 8 or 16 lanes");
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror: lane i of 8 reads lane 7 - i
+    if constexpr (G == 16) v += dpp<0x140>(v);  // row_mirror: lane i of 16 reads lane 15 - i
     return v;
 }
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 constexpr uint32_t kOOB = 0x80000000u;  // any offset past a buffer resource reads zero
 
@@ -140,7 +161,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     constexpr int PASS = NW * RW;      // positions per pass
     constexpr int HALF = HD / 2;
     __shared__ float qs[HD], kn[HD], vn[HD], redm[NW], reds[NW];
-    __shared__ float accs[NW][HD];
+    __shared__ float accs[NW][4][HD];
     const int hd = blockIdx.x / S, sp = blockIdx.x % S, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int pos = *pos_p;
     const int T = pos + 1, P = (T + S - 1) / S;
@@ -187,8 +208,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     float s_new = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_new = fmaf(qv[e], kn[ch * 8 + e], s_new);
-#pragma unroll
-    for (int o = 1; o < CH; o <<= 1) s_new += __shfl_xor(s_new, o, 64);
+    s_new = group_sum<CH>(s_new);
 
     const float scale = 1.0f / sqrtf((float)HD);
     float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
@@ -208,8 +228,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
             widen8(kr[i], f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) sc = fmaf(qv[e], f[e], sc);
-#pragma unroll
-            for (int o = 1; o < CH; o <<= 1) sc += __shfl_xor(sc, o, 64);
+            sc = group_sum<CH>(sc);
             const int row = base + i * RPI + rl;
             sc = row == pos ? s_new : sc;
             sv[i] = row < r1 ? sc * scale : -__builtin_inff();
@@ -251,21 +270,25 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
         m_run = m_new;
         __syncthreads();  // redm / reds are rewritten by the next pass
     }
-    // sum P.V partials over the lanes holding the same chunk, then over waves
+    // sum P.V partials over the lanes holding the same chunk: within a 16-lane
+    // row (HD = 64: two rows of 8 chunks, row_ror 8 pairs lane i with i + 8),
+    // then over the four rows of each wave and over waves in LDS
+    if constexpr (CH == 8) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+        for (int e = 0; e < 8; ++e) acc[e] += dpp<0x128>(acc[e]);
+    }
+    if ((lane & 15) < CH) {
 #pragma unroll
-        for (int o = CH; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o, 64);
-    if (rl == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) accs[w][ch * 8 + e] = acc[e];
+        for (int e = 0; e < 8; ++e) accs[w][lane >> 4][ch * 8 + e] = acc[e];
     }
     __syncthreads();
     const size_t slot = (size_t)hd * S + sp;
     if (t < HD) {
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NW; ++i) sum += accs[i][t];
+        for (int i = 0; i < NW; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum += accs[i][j][t];
         part[slot * HD + t] = sum;
     }
     if (t == 0) ml[slot] = make_float2(m_run, l_run);
