@@ -28,6 +28,7 @@
 #include <math.h>
 
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -326,6 +327,12 @@ __global__ __launch_bounds__(AT) void k_argmax_embed(const float *__restrict__ l
     __shared__ int bi[AT / 64];
     __shared__ int next_s;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // position, prompt length and the prompt's next token are requested
+    // before the scan, off the block's tail
+    const int pos = *pos_p;
+    const int n_prompt = *n_prompt_p;
+    const bool teacher = pos + 1 < n_prompt;
+    const int forced = teacher ? tokens[pos + 1] : 0;
     float best = -1e9f;
     int idx = 0;
     // each thread scans its indices in ascending order (strict >: the first
@@ -353,28 +360,38 @@ __global__ __launch_bounds__(AT) void k_argmax_embed(const float *__restrict__ l
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
+    // (value, index) pairs combine by the larger value, then the smaller index:
+    // a total order, so any reduction tree picks the scan's answer
+    auto take = [&](float ov, int oi) {
         if (ov > best || (ov == best && oi < idx)) {
             best = ov;
             idx = oi;
         }
+    };
+    auto dpp_step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        take(dpp<C>(best), __builtin_amdgcn_update_dpp(0, idx, C, 0xF, 0xF, false));
+    };
+    dpp_step(std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+    dpp_step(std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+    dpp_step(std::integral_constant<int, 0x141>{});  // row_half_mirror
+    dpp_step(std::integral_constant<int, 0x140>{});  // row_mirror: each 16-lane row holds its pick
+    {
+        const float v0 = best;
+        const int i0 = idx;
+        best = readlane(v0, 0);
+        idx = __builtin_amdgcn_readlane(i0, 0);
+#pragma unroll
+        for (int r = 16; r < 64; r += 16) take(readlane(v0, r), __builtin_amdgcn_readlane(i0, r));
     }
     if (lane == 0) {
         bv[wave] = best;
         bi[wave] = idx;
     }
     __syncthreads();
-    const int pos = *pos_p;
     if (t == 0) {
-        for (int w = 1; w < AT / 64; ++w)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
-                best = bv[w];
-                idx = bi[w];
-            }
-        const int next = pos + 1 < *n_prompt_p ? tokens[pos + 1] : idx;
+        for (int w = 1; w < AT / 64; ++w) take(bv[w], bi[w]);
+        const int next = teacher ? forced : idx;
         tokens[pos + 1] = next;
         next_s = next;
     }
