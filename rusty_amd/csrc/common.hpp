@@ -97,7 +97,7 @@ int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const voi
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
                               float eps, void *h, hipStream_t s);
 // y[n] += sum_k W[n, k] x[k] (m = 1, f32 y) with x the decode attention output
-// combined in the prologue from n_split (1, 2 or 4) partial softmaxes per head
+// combined in the prologue from n_split (1, 2, 4 or 8) partial softmaxes per head
 // of head_dim elements: partials = acc[head][n_split][head_dim] f32, then
 // (m, l)[head][n_split] float2.
 int launch_gemv_decode_attn_add(const rq_qweight &w, const float *partials, int n_split, int head_dim, float *y,

@@ -445,6 +445,7 @@ Decode pick_fmt(int fmt, bool norm, bool tall, int sa) {
         if (sa == 1) return inst<1, CPT, TPR, 4, 0, false, false, 1>();
         if (sa == 2) return inst<1, CPT, TPR, 4, 0, false, false, 2>();
         if (sa == 4) return inst<1, CPT, TPR, 4, 0, false, false, 4>();
+        if (sa == 8) return inst<1, CPT, TPR, 4, 0, false, false, 8>();
         if (fmt == 2) return norm ? inst<1, CPT, TPR, RSN, 0, true, true>() : inst<1, CPT, TPR, 2, 0, true, false>();
         if (fmt == 0 && tall) return norm ? inst<1, CPT, TPR, 8, 0, false, true>() : inst<1, CPT, TPR, 8, 0, false, false>();
         if (norm) return inst<1, CPT, TPR, RN, 0, false, true>();
@@ -491,7 +492,7 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     if (w2 && (w.format != RQ_Q_ROWWISE_I8 || w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16)))
         return RQ_ERR_UNSUPPORTED;
     if (nw && (m != 1 || w.format != RQ_Q_ROWWISE_I8 || !aligned(nw, 16))) return RQ_ERR_UNSUPPORTED;
-    if (sa && (m != 1 || w2 || nw || w.format != RQ_Q_ROWWISE_I8 || (sa != 1 && sa != 2 && sa != 4) ||
+    if (sa && (m != 1 || w2 || nw || w.format != RQ_Q_ROWWISE_I8 || (sa != 1 && sa != 2 && sa != 4 && sa != 8) ||
                attn_hd < 8 || attn_hd % 8 != 0 || K % attn_hd != 0))
         return RQ_ERR_UNSUPPORTED;
     const int C = (int)(K / 16);
