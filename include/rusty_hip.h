@@ -176,6 +176,19 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
 int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
                   rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream);
 
+/* No counterpart in the reference: rq_mlp_swiglu for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  Same kernels and results as rq_mlp_swiglu, but the
+ * intermediate h lives in a library-owned device array of 8 MiB per device
+ * (held until the process ends) instead of a caller workspace, so the call
+ * allocates nothing; the prefill GEMMs of this variant do not split K.
+ * Limit: 4 * m * intermediate <= 8 MiB (m * intermediate <= 2,097,152), else
+ * RQ_ERR_SHAPE.  All calls on one device share that device's array: calls
+ * that overlap on one device (other streams, other threads) race and must be
+ * serialised by the caller. */
+int rq_mlp_swiglu_noalloc(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down,
+                          const void *x, rq_dtype x_dtype, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream);
+
 /* Input gradient through a frozen quantized Linear (LoRA fine-tuning):
  * dX[m, k_in] = dY[m, n_out] . deq(W).  The `grad_a = matmul_bt(grad, b)`
  * step of MatMulNode::backward (rusty-autograd/src/lib.rs:152-158) with b the

@@ -106,6 +106,8 @@ _SIGNATURES = {
     "rq_qmatmul": [_P, POINTER(rq_qweight), _P, c_int, _P, c_int, c_int64, _P],
     "rq_mlp_swiglu": [_P, POINTER(rq_qweight), POINTER(rq_qweight), POINTER(rq_qweight), _P, c_int, _P, _P, c_int,
                       c_int64, _P],
+    "rq_mlp_swiglu_noalloc": [_P, POINTER(rq_qweight), POINTER(rq_qweight), POINTER(rq_qweight), _P, c_int, _P,
+                              c_int, c_int64, _P],
     "rq_qmatmul_dx": [_P, POINTER(rq_qweight), _P, c_int, _P, c_int, c_int64, _P],
     "rq_llama_create": [_P, POINTER(rq_llama_config), POINTER(rq_llama_weights), POINTER(c_void_p)],
     "rq_llama_destroy": [_P],

@@ -137,6 +137,7 @@ int rq_ctx_create(int device, rq_ctx **out) {
         }
         (void)hipGetLastError();  // a failed optional allocation is not the caller's error
     }
+    noalloc_init(device);  // the no-alloc SwiGLU's scratch address on this device
     *out = ctx;
     return RQ_OK;
 }
@@ -338,6 +339,51 @@ int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dty
     return launch_qlinear_generic(w, x, xt, y, yt, m, s);
 }
 
+// Argument checks shared by rq_mlp_swiglu and its no-alloc variant (pointers
+// are checked by the callers).
+int rq::swiglu_check(const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, rq_dtype x_dtype,
+                     rq_dtype y_dtype, int64_t m) {
+    int st;
+    if ((st = check_qweight(gate)) != RQ_OK || (st = check_qweight(up)) != RQ_OK || (st = check_qweight(down)) != RQ_OK)
+        return st;
+    if ((x_dtype != RQ_F16 && x_dtype != RQ_F32) || (y_dtype != RQ_F16 && y_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    const int64_t I = gate->n_out, H = gate->k_in;
+    if (up->n_out != I || up->k_in != H || down->n_out != H || down->k_in != I)
+        return fail(RQ_ERR_SHAPE, "SwiGLU shapes: gate/up [%lld,%lld], down must be [%lld,%lld]", (long long)I,
+                    (long long)H, (long long)H, (long long)I);
+    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
+    int64_t t;
+    if (!mul_ok(m, 2 * I, &t) || !mul_ok(m, H, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
+    return RQ_OK;
+}
+
+// The SwiGLU MLP over validated arguments, h a workspace of 2*m*I fp16 values:
+// the gate/up pass writes h = silu(g) * u into its first m*I values (the
+// prefill path stages g and u in its two halves first), then the down
+// projection reads it.  ws: the split-K workspace the prefill GEMMs may use.
+int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, const rq_qweight &down, const void *x,
+                   rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, const GemmWorkspace &ws,
+                   hipStream_t s) {
+    const int64_t I = gate.n_out;
+    int st = RQ_ERR_UNSUPPORTED;
+    if (x_dtype == RQ_F16 && m <= 2) st = launch_swiglu_decode(gate, up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 16) st = launch_swiglu_mfma(gate, up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(gate, up, x, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && m > 16) {
+        // prefill: gate and up through the GEMM into the two halves of the
+        // workspace, then h = silu(g) * u in place over the first half
+        _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
+        st = launch_gemm(gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, ws, s);
+        if (st == RQ_OK) st = launch_gemm(up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, ws, s);
+        if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
+    }
+    if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(gate, up, x, x_dtype, h, m, s);
+    if (st != RQ_OK) return st;
+    // down projection of h
+    return qmatmul_dispatch(ctx, down, h, RQ_F16, y, y_dtype, m, s);
+}
+
 extern "C" {
 
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y, rq_dtype y_dtype,
@@ -358,38 +404,11 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
 int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,
                   rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, rq_stream stream) {
     RQ_ENTER(ctx);
-    int st;
-    if ((st = check_qweight(gate)) != RQ_OK || (st = check_qweight(up)) != RQ_OK || (st = check_qweight(down)) != RQ_OK)
-        return st;
-    if ((x_dtype != RQ_F16 && x_dtype != RQ_F32) || (y_dtype != RQ_F16 && y_dtype != RQ_F32))
-        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
-    const int64_t I = gate->n_out, H = gate->k_in;
-    if (up->n_out != I || up->k_in != H || down->n_out != H || down->k_in != I)
-        return fail(RQ_ERR_SHAPE, "SwiGLU shapes: gate/up [%lld,%lld], down must be [%lld,%lld]", (long long)I,
-                    (long long)H, (long long)H, (long long)I);
-    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
-    int64_t t;
-    if (!mul_ok(m, 2 * I, &t) || !mul_ok(m, H, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
-    if (m == 0 || H == 0) return RQ_OK;
-    if (!y || !h || (H > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation or workspace pointer");
+    int st = swiglu_check(gate, up, down, x_dtype, y_dtype, m);
+    if (st != RQ_OK || m == 0 || gate->k_in == 0) return st;
+    if (!y || !h || !x) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation or workspace pointer");
     hipStream_t s = pick(ctx, stream);
-    // gate/up pass -> h (fp16, [m, I])
-    st = RQ_ERR_UNSUPPORTED;
-    if (x_dtype == RQ_F16 && m <= 2) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
-    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 16) st = launch_swiglu_mfma(*gate, *up, x, h, (int)m, s);
-    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(*gate, *up, x, h, (int)m, s);
-    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m > 16) {
-        // prefill: gate and up through the GEMM into the two halves of the
-        // workspace, then h = silu(g) * u in place over the first half
-        _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
-        st = launch_gemm(*gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, gemm_workspace(ctx, s), s);
-        if (st == RQ_OK) st = launch_gemm(*up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, gemm_workspace(ctx, s), s);
-        if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
-    }
-    if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(*gate, *up, x, x_dtype, h, m, s);
-    if (st != RQ_OK) return st;
-    // down projection of h
-    return qmatmul_dispatch(ctx, *down, h, RQ_F16, y, y_dtype, m, s);
+    return swiglu_run(ctx, *gate, *up, *down, x, x_dtype, h, y, y_dtype, m, gemm_workspace(ctx, s), s);
 }
 
 int rq_qmatmul_dx(rq_ctx *ctx, const rq_qweight *w, const void *dy, rq_dtype dy_dtype, void *dx, rq_dtype dx_dtype,

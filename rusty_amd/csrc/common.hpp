@@ -114,6 +114,19 @@ int launch_qmatmul_dx(const rq_qweight &w, const void *dy, rq_dtype dyt, void *d
 int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
                      hipStream_t s);
 
+// SwiGLU MLP: argument checks (weights, dtypes, shapes) and the launches over
+// a workspace h of 2*m*I fp16 values (see rq_mlp_swiglu).
+int swiglu_check(const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, rq_dtype x_dtype,
+                 rq_dtype y_dtype, int64_t m);
+int swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, const rq_qweight &down, const void *x,
+               rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, const GemmWorkspace &ws,
+               hipStream_t s);
+
+// Looks up this device's copy of the no-alloc entry point's scratch array
+// (once per device; `device` must be current).  A failure is recorded and
+// reported by that entry point, not by context creation.
+void noalloc_init(int device);
+
 enum MatmulVariant { MM_AB = 0, MM_ABT = 1, MM_ATB = 2 };
 
 }  // namespace rq
