@@ -3,16 +3,18 @@
 
 Headline (BASELINE.json `metric`, configs[1]): decode dequant-GEMV, W int8
 [4096, 4096] with per-row f32 scales, X fp16 [1, 4096], Y fp16.  One step is
-one GEMV over one weight copy; 48 distinct copies (806 MB, > 2x the 256 MB
-Infinity Cache) rotate so every step reads its weight from HBM.  Steps are
-replayed from a HIP graph of 48 launches (remainder launched directly), all
-on the context's stream.
+one GEMV over one weight copy; 96 distinct copies (1.6 GB, > 6x the 256 MB
+Infinity Cache) rotate so every step reads its weight from HBM.  The timed
+region is exactly `--steps` launches, replayed from HIP graphs on the context's
+stream (see time_steps).
 
 Printed JSON (one line, stdout):
   value            whole-job GB/s = algorithmic bytes x steps / timed wall time
   roofline         dominant kernel (the GEMV): algorithmic bytes / mean launch
-                   duration (HIP events around the timed region on the launch
-                   stream, launches back to back), vs 8 TB/s
+                   duration (device wall-clock stamps on the launch stream
+                   around the timed launches, back to back), vs 8 TB/s
+  floor            the same weight bytes read without the GEMV's arithmetic
+                   (and with its output store): the one-launch floor
   cpu_baseline     the reference's per-token path on host cores: k-ascending
                    f32 GEMV on the load-time-dequantized f32 weight (oracle port)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
@@ -38,7 +40,7 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
-COPIES = 48
+COPIES = 96
 METRIC = "int8 GEMV GB/s (% HBM peak) at 4096² M=1; prefill TFLOPS; decode tok/s"
 
 
@@ -83,43 +85,136 @@ class GemvWorkload:
             _lib.check(st, "rq_qmatmul")
 
 
-def time_steps(ctx, wl: GemvWorkload, steps: int, warmup: int, use_graph: bool = True) -> float:
-    """Times exactly `steps` launches on the context stream; returns elapsed ms.
+class DeviceClock:
+    """Two device timestamps (rq_device_clock: the device's constant-rate wall
+    clock stored by a one-wave kernel on the stream) that can sit inside a
+    captured graph, around exactly the launches to be timed."""
 
-    With the HIP graph the launches run back to back (rocprofv3 shows no gap
-    between consecutive dispatches), so elapsed / steps is the mean kernel
-    duration as well as the whole-job time per step."""
+    def __init__(self, ctx):
+        from rusty_amd import DType, UnifiedTensor, _lib
+
+        self.ctx = ctx
+        self.buf = UnifiedTensor.new(ctx, np.zeros(2, np.uint64).view(np.uint8), dtype=DType.U8)
+        hz = ctypes.c_uint64()
+        _lib.call("rq_device_clock", ctx.handle, self.buf.ptr, ctypes.byref(hz), None)
+        ctx.sync()
+        self.hz = hz.value
+
+    def stamp(self, i: int) -> None:
+        from rusty_amd import _lib
+
+        _lib.call("rq_device_clock", self.ctx.handle, self.buf.ptr + 8 * i, None, None)
+
+    def elapsed_ms(self) -> float:
+        t = self.buf.to_vec().view(np.uint64)
+        return float(int(t[1]) - int(t[0])) / self.hz * 1e3
+
+
+class ProbeWorkload:
+    """The headline GEMV's weight stream without its arithmetic (rq_stream_probe
+    over the same rotating copies, same grid: 2 rows of 4096 B per block of
+    256 threads, one 16-byte non-temporal load per thread and row); with
+    `store`, one 2-byte value per row is written, as the GEMV writes Y."""
+
+    def __init__(self, wl: GemvWorkload, store: bool):
+        from rusty_amd import _lib
+
+        self.wl, self.copies, self.store = wl, wl.copies, store
+        self._fn = _lib.lib().rq_stream_probe
+        self._h = wl.ctx.handle
+        self.bytes = wl.n * wl.k + (2 * wl.n if store else 0)
+
+    def launch(self, i: int) -> None:
+        wl = self.wl
+        st = self._fn(self._h, wl.codes.ptr + (i % self.copies) * wl.n * wl.k, wl.k, wl.n, 2, wl.y.ptr,
+                      1 if self.store else 0, None)
+        if st != 0:
+            from rusty_amd import _lib
+            _lib.check(st, "rq_stream_probe")
+
+
+def floor_probe(ctx, wl: GemvWorkload, steps: int, use_graph: bool = True) -> dict:
+    """Mean launch time of the headline GEMV beside the bare read of its weight
+    bytes and the read plus its output store, each over the same rotating
+    copies and timed the same way: the one-launch floor the GEMV sits on."""
+    out = {}
+    for name, w in (("gemv", wl), ("read", ProbeWorkload(wl, False)), ("read_store", ProbeWorkload(wl, True))):
+        ms, _ = time_steps(ctx, w, steps, wl.copies, use_graph=use_graph)
+        out[f"{name}_us"] = round(ms / steps * 1e3, 3)
+    out["gemv_over_read_store"] = round(out["gemv_us"] / out["read_store_us"], 4)
+    out["read_gbs"] = round(wl.n * wl.k / (out["read_us"] * 1e-6) / 1e9, 1)
+    out["what"] = ("16 MiB weight read by rq_stream_probe with the GEMV's grid (2048 blocks x 256 threads, 2 rows "
+                   "each), without and with the 8 KB output store, vs the GEMV itself; same copies, same timing")
+    return out
+
+
+def time_steps(ctx, wl, steps: int, warmup: int, use_graph: bool = True):
+    """Times exactly `steps` launches on the context stream; returns
+    (elapsed ms, description of what the timed region launched).
+
+    Graph mode: one captured graph holds an untimed rotation over all `copies`
+    weight copies, a device timestamp, `steps` launches over copies 0, 1, ...
+    (mod copies), and a second timestamp.  Both timestamps are kernels on the
+    launch stream inside the graph (rq_device_clock), so the timed region is
+    exactly the `steps` dispatches, back to back, plus one kernel boundary,
+    with neither the graph's launch nor the host in it; the lead-in rotation
+    keeps the device at its sustained clock and leaves copy 0 the least
+    recently used.  elapsed / steps is the mean kernel duration as well as the
+    whole-job time per step.  (HIP events cannot be graph nodes here; events
+    around a graph of 20 launches read 5.3 us per launch where 2000 read 4.7,
+    the difference being the graph launch's own cost, which time_steps also
+    reports as `graph_launch_ms`.)  Direct mode (tracers that do not follow
+    graph launches): batches of `copies` launches, each queued behind a device
+    delay, between HIP events; the timed region then includes the delays."""
     from rusty_amd.hiprt import Event, Graph
 
     stream = ctx.stream
-    graph = Graph(stream, lambda: [wl.launch(i) for i in range(wl.copies)]) if use_graph else None
+    C = wl.copies
+    t0, t1 = Event(), Event()
+    if use_graph:
+        clock = DeviceClock(ctx)
+        rotation = Graph(stream, lambda: [wl.launch(i) for i in range(C)])
 
-    def run(n: int) -> None:
-        i = 0
-        if graph is not None:
-            while n - i >= wl.copies:
-                graph.launch()
-                i += wl.copies
-        while i < n:
-            if graph is None and i % wl.copies == 0:  # direct: queue the batch behind a device delay
-                device_delay(ctx, HOST_US_PER_LAUNCH * min(wl.copies, n - i))
-            wl.launch(i)
-            i += 1
+        def body():
+            for i in range(C):
+                wl.launch(i)
+            clock.stamp(0)
+            for i in range(steps):
+                wl.launch(i)
+            clock.stamp(1)
+
+        timed = Graph(stream, body)
+        desc = (f"one HIP graph: an untimed rotation over all {C} weight copies, then {steps} launches over copies "
+                f"0, 1, ... (mod {C}) between two device wall-clock stamps on the launch stream")
+    else:
+        rotation = _Direct(ctx, lambda: [wl.launch(i) for i in range(C)], C)
+        q, r = divmod(steps, C)
+        batches = [rotation] * q + ([_Direct(ctx, lambda: [wl.launch(i) for i in range(r)], r)] if r else [])
+        desc = (f"direct launches in batches of <= {C}, each batch queued behind a device delay, between HIP "
+                f"events (for tracers; the timed region includes the delays)")
 
     # W warm-up steps, and at least 0.25 s of them: the clock ramps out of
     # idle over tens of ms, and the timed steps should see the sustained clock
-    run(warmup)
+    for _ in range(max(1, -(-warmup // C))):
+        rotation.launch()
     ctx.sync()
     t_end = time.perf_counter() + 0.25
     while time.perf_counter() < t_end:
-        run(max(wl.copies, 1))
+        rotation.launch()
         ctx.sync()
-    t0, t1 = Event(), Event()
     t0.record(stream)
-    run(steps)
+    if use_graph:
+        timed.launch()
+    else:
+        for b in batches:
+            b.launch()
     t1.record(stream)
     t1.synchronize()
-    return t0.elapsed_ms(t1)
+    events_ms = t0.elapsed_ms(t1)
+    if not use_graph:
+        return events_ms, desc
+    time_steps.graph_launch_ms = round(events_ms, 4)  # whole graph launch incl. the rotation, for reference
+    return clock.elapsed_ms(), desc
 
 
 HOST_US_PER_LAUNCH = 80  # generous host cost of one direct launch under a tracer
@@ -146,10 +241,41 @@ class _Direct:
         self.fn()
 
 
+def _replays(ctx, fn, launches: int, use_graph: bool, reps: int = 3) -> list:
+    """Elapsed ms of `reps` timed runs of the work `fn` enqueues, after >= 0.25 s
+    of warm-up runs.  Graph mode: fn is captured between two device
+    wall-clock stamps (rq_device_clock), so each timed run is exactly fn's
+    dispatches, back to back, without the graph launch; each run starts after a
+    host wait (a burst, as a prompt arrives).  Direct mode: fn's launches
+    queued behind a device delay, between HIP events."""
+    from rusty_amd.hiprt import Event, Graph
+
+    if use_graph:
+        clock = DeviceClock(ctx)
+
+        def body():
+            clock.stamp(0)
+            fn()
+            clock.stamp(1)
+        graph = Graph(ctx.stream, body)
+    else:
+        a, b = Event(), Event()
+        graph = _Direct(ctx, lambda: (a.record(ctx.stream), fn(), b.record(ctx.stream)), launches)
+    t_end = time.perf_counter() + 0.25
+    while time.perf_counter() < t_end:
+        graph.launch()
+        ctx.sync()
+    times = []
+    for _ in range(reps):
+        graph.launch()
+        ctx.sync()
+        times.append(clock.elapsed_ms() if use_graph else a.elapsed_ms(b))
+    return times
+
+
 def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5,
             use_graph: bool = True):
     from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
-    from rusty_amd.hiprt import Event, Graph
 
     g = synth.rng(n + k)
     q, s = synth.rowwise_weight(g, n, k)
@@ -159,23 +285,14 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
     # the launches are replayed from a HIP graph: back to back on the device,
     # with no host call in between (a Python call per launch costs ~40 us).
     # Warm-up is time-based (>= 0.25 s of replays) so the timed replays run at
-    # the sustained clock, not the ramp out of idle; median of 3 replays.
+    # the sustained clock, not the ramp out of idle; median of 3 replays, each
+    # a burst after a host wait (back-to-back replays with no wait measured
+    # ~6 % slower at 2048x4096x4096: the MFMA clock is power-limited).
     for _ in range(warmup):
         engine.qmatmul(ctx, x, w, y)
     fn = lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(steps)]  # noqa: E731
-    graph = Graph(ctx.stream, fn) if use_graph else _Direct(ctx, fn, steps)
-    t_end = time.perf_counter() + 0.25
-    while time.perf_counter() < t_end:
-        graph.launch()
-        ctx.sync()
-    times = []
-    for _ in range(3):
-        a, b = Event(), Event()
-        a.record(ctx.stream)
-        graph.launch()
-        b.record(ctx.stream)
-        b.synchronize()
-        times.append(a.elapsed_ms(b) / steps)
+    times = _replays(ctx, fn, steps, use_graph)
+    times = [t / steps for t in times]
     ms = sorted(times)[1]
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     return {"shape": f"{m}x{n}x{k}", "ms": round(ms, 5), "tflops": round(tflops, 2),
@@ -187,7 +304,6 @@ def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60, use_graph: 
     down int8 [4096,11008], per-row scales; x fp16 [m,4096].  Bytes per MLP =
     3*I*H codes + 4*(2I+H) scales + 2mH (x) + 2*2mI (h written, read) + 4mH (y f32)."""
     from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
-    from rusty_amd.hiprt import Event, Graph
 
     I, H = 11008, 4096
     g = synth.rng(2)
@@ -202,19 +318,7 @@ def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60, use_graph: 
     # replayed from a HIP graph (no host call between MLPs), after >= 0.25 s
     # of warm-up replays; median of 3 timed replays
     fn = lambda: [engine.mlp_swiglu(ctx, x, *mats[i % copies], y, h) for i in range(launches)]  # noqa: E731
-    graph = Graph(ctx.stream, fn) if use_graph else _Direct(ctx, fn, 2 * launches)
-    t_end = time.perf_counter() + 0.25
-    while time.perf_counter() < t_end:
-        graph.launch()
-        ctx.sync()
-    times = []
-    for _ in range(3):
-        a, b = Event(), Event()
-        a.record(ctx.stream)
-        graph.launch()
-        b.record(ctx.stream)
-        b.synchronize()
-        times.append(a.elapsed_ms(b) / launches * 1e3)
+    times = [t / launches * 1e3 for t in _replays(ctx, fn, 2 * launches, use_graph)]
     us = sorted(times)[1]
     nbytes = 3 * I * H + 4 * (2 * I + H) + 2 * m * H + 2 * 2 * m * I + 4 * m * H
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -305,9 +409,9 @@ def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
     extra = {}
     for m, n, k in ((4, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 11008, 4096), (1, 4096, 11008),
                     (8, 4096, 11008)):
-        copies = max(2, min(COPIES, (600 << 20) // (n * k)))
+        copies = max(2, min(COPIES, (1200 << 20) // (n * k)))
         w2 = GemvWorkload(ctx, m, n, k, copies=copies)
-        wms = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
+        wms, _ = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
         kms = wms / (20 * copies)
         extra[f"m{m}_{n}x{k}"] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1),
                                   "us_per_launch": round(kms * 1e3, 2),
@@ -329,7 +433,7 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps as direct launches instead of one graph per token (for tools that "
@@ -352,6 +456,8 @@ def main() -> int:
         out = {"only": args.only}
         if args.only == "gemv":
             out["decode_gemv"] = decode_gemv_extra(ctx, use_graph=not args.no_graph)
+        elif args.only == "floor":
+            out["floor"] = floor_probe(ctx, GemvWorkload(ctx, 1, 4096, 4096), args.steps, use_graph=not args.no_graph)
         elif args.only == "prefill":
             out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph)
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
@@ -366,7 +472,7 @@ def main() -> int:
 
     wl = GemvWorkload(ctx, 1, 4096, 4096)
     log("headline: GEMV 4096x4096 M=1, %d rotating copies" % wl.copies)
-    wall_ms = time_steps(ctx, wl, args.steps, args.warmup, use_graph=not args.no_graph)
+    wall_ms, launch_desc = time_steps(ctx, wl, args.steps, args.warmup, use_graph=not args.no_graph)
     ms_per_step = wall_ms / args.steps
     value = wl.bytes * args.steps / (wall_ms * 1e-3) / 1e9
     kern_ms = ms_per_step  # back-to-back graph launches: mean launch duration
@@ -386,19 +492,24 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8 weights x fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded numpy PCG64: int8 codes U[-127,127], scales U(0.001,0.02), X ~ N(0,1) fp16)",
-        "config": {"workload": "configs[1]: decode dequant-GEMV W int8 [4096,4096] per-row f32 scale, "
-                               "X fp16 [1,4096], Y fp16; 48 rotating weight copies (806 MB > 2x MALL)",
-                   "m": 1, "n": 4096, "k": 4096, "bytes_per_step": wl.bytes,
-                   "launch": ("direct, batches of 48 queued behind a device delay (for tracers; the timed "
-                              "region includes the delays)") if args.no_graph else "HIP graph of 48 launches"},
+        "config": {"workload": (f"configs[1]: decode dequant-GEMV W int8 [4096,4096] per-row f32 scale, "
+                                f"X fp16 [1,4096], Y fp16; {wl.copies} weight copies "
+                                f"({wl.copies * wl.n * wl.k / 1e9:.2f} GB > 256 MB MALL), timed steps "
+                                f"touch min(steps, {wl.copies}) of them"),
+                   "m": 1, "n": 4096, "k": 4096, "bytes_per_step": wl.bytes, "launch": launch_desc},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile("k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>"),
                      "kernel": "k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>",
                      "mean_launch_us": round(kern_ms * 1e3, 3),
-                     "timing": "HIP events around the timed region on the launch stream / steps"},
+                     "timing": ("device wall clock (rq_device_clock, 100 MHz) stamped on the launch stream "
+                                "before and after the timed launches inside one graph, / steps"
+                                if not args.no_graph else "HIP events around the timed region / steps"),
+                     "graph_launch_ms_with_events": getattr(time_steps, "graph_launch_ms", None)},
     }
 
+    result["floor"] = floor_probe(ctx, wl, args.steps, use_graph=not args.no_graph)
+    log(f"floor {result['floor']}")
     if not args.quick:
         result["decode_gemv"] = decode_gemv_extra(ctx)
         pf = []

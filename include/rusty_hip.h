@@ -85,6 +85,25 @@ int rq_sync(rq_ctx *ctx, rq_stream stream);
  * graph launches) -- work enqueued behind the delay queues up on the device and
  * then runs back to back, as it does when replayed from a graph. */
 int rq_device_delay(rq_ctx *ctx, uint32_t microseconds, rq_stream stream);
+/* A measurement aid with no counterpart in the reference: a one-wave kernel
+ * stores the device's constant-rate wall clock (a 64-bit tick count) to the
+ * device address dst when `stream` reaches it; *ticks_per_second (if not NULL)
+ * receives the clock's rate on return.  Unlike HIP events it may be captured
+ * in a HIP graph, so a region inside one graph launch can be timed. */
+int rq_device_clock(rq_ctx *ctx, uint64_t *dst, uint64_t *ticks_per_second, rq_stream stream);
+/* A measurement aid with no counterpart in the reference: the decode GEMV's
+ * weight stream without its arithmetic.  Reads `rows` rows of `row_bytes`
+ * bytes (a multiple of 16, at most 16384) at `src` (16-byte aligned) with the
+ * GEMV's grid (blocks of 256 threads, `rows_per_block` rows each, 1..4; every
+ * thread loads 16-byte chunks of each row, non-temporal) and XOR-combines each
+ * wave's words.  store != 0: lane 0 of wave r stores the combined value of
+ * row r of its block (folded to 2 bytes) to dst[row] -- the GEMV's fp16
+ * output; store == 0: dst[row] is written only if that value is all ones
+ * (never, in practice), so the loads are consumed and nothing is stored.  dst
+ * holds `rows` 2-byte values.  Timed beside the GEMV it gives the one-launch
+ * read (and read + store) floor for the same bytes. */
+int rq_stream_probe(rq_ctx *ctx, const void *src, size_t row_bytes, size_t rows, int rows_per_block, void *dst,
+                    int store, rq_stream stream);
 /* Human-readable name of a status code, and the calling thread's last error
  * message (empty string if none). */
 const char *rq_status_string(int status);

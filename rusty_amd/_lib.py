@@ -89,6 +89,8 @@ _SIGNATURES = {
     "rq_ctx_num_cus": [_P, POINTER(c_int)],
     "rq_sync": [_P, _P],
     "rq_device_delay": [_P, c_uint32, _P],
+    "rq_stream_probe": [_P, _P, c_size_t, c_size_t, c_int, _P, c_int, _P],
+    "rq_device_clock": [_P, _P, POINTER(ctypes.c_uint64), _P],
     "rq_status_string": [c_int],
     "rq_last_error": [],
     "rq_alloc": [_P, c_size_t, POINTER(c_void_p)],

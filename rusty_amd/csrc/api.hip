@@ -63,6 +63,68 @@ __global__ void k_device_delay(uint64_t ticks) {
     while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(32);
 }
 
+// One lane stores the device's constant-rate wall clock when the stream
+// reaches this launch.
+__global__ void k_device_clock(uint64_t *dst) {
+    if (threadIdx.x == 0) *dst = wall_clock64();
+}
+
+// Measurement aid: the weight stream of the decode GEMV without its
+// arithmetic.  Block b reads rows [b*R, b*R + R) of `rows` rows of row_bytes
+// bytes; thread t reads 16-byte chunks t, t + 256, ... (CPT of them) of each
+// row with the non-temporal policy, like the GEMV's weight loads (all in
+// flight, then combined).  Each wave XOR-reduces its lanes' words with DPP
+// steps, so every lane's loads feed the result; with store, lane 0 of wave
+// r < R stores it (folded to 2 bytes) for row b*R + r, as the GEMV stores its
+// fp16 output; without, it is stored only if it equals an all-ones word (never,
+// in practice), so the loads stay live and nothing is written.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int R, int CPT>
+__global__ __launch_bounds__(256) void k_stream_probe(const uint8_t *__restrict__ src, int row_bytes, int rows,
+                                                      uint16_t *__restrict__ dst, int store) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int row0 = blockIdx.x * R, rows_here = min(R, rows - row0);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src) + (size_t)row0 * row_bytes, 0,
+                                                      (uint32_t)(rows_here * row_bytes), 0x00020000);
+    const int C = row_bytes / 16;
+    u32x4 v[R][CPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = t + 256 * j;  // rows past the resource read as zero
+            v[r][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rs, c < C ? (uint32_t)(r * row_bytes + c * 16) : 0x80000000u, 0, 2));
+        }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) acc ^= v[r][j].x ^ v[r][j].y ^ v[r][j].z ^ v[r][j].w;
+    acc ^= dpp_u32<0xB1>(acc);   // quad_perm [1,0,3,2]
+    acc ^= dpp_u32<0x4E>(acc);   // quad_perm [2,3,0,1]
+    acc ^= dpp_u32<0x141>(acc);  // row_half_mirror
+    acc ^= dpp_u32<0x140>(acc);  // row_mirror: each 16-lane row holds its XOR
+    acc = (uint32_t)__builtin_amdgcn_readlane((int)acc, 0) ^ (uint32_t)__builtin_amdgcn_readlane((int)acc, 16) ^
+          (uint32_t)__builtin_amdgcn_readlane((int)acc, 32) ^ (uint32_t)__builtin_amdgcn_readlane((int)acc, 48);
+    if (lane == 0 && wave < rows_here && (store || acc == 0xFFFFFFFFu)) dst[row0 + wave] = (uint16_t)(acc ^ (acc >> 16));
+}
+
+template <int R>
+void launch_probe(int cpt, unsigned blocks, hipStream_t s, const uint8_t *src, int row_bytes, int rows, uint16_t *dst,
+                  int store) {
+    switch (cpt) {
+    case 1: hipLaunchKernelGGL((k_stream_probe<R, 1>), dim3(blocks), dim3(256), 0, s, src, row_bytes, rows, dst, store); break;
+    case 2: hipLaunchKernelGGL((k_stream_probe<R, 2>), dim3(blocks), dim3(256), 0, s, src, row_bytes, rows, dst, store); break;
+    case 3: hipLaunchKernelGGL((k_stream_probe<R, 3>), dim3(blocks), dim3(256), 0, s, src, row_bytes, rows, dst, store); break;
+    default: hipLaunchKernelGGL((k_stream_probe<R, 4>), dim3(blocks), dim3(256), 0, s, src, row_bytes, rows, dst, store); break;
+    }
+}
+
 // Byte fill: 16-byte stores over the aligned middle (grid-stride), single
 // bytes for the unaligned head and tail.  A kernel rather than
 // hipMemsetAsync, so that a caller may capture it in a HIP graph: memset
@@ -182,6 +244,44 @@ int rq_device_delay(rq_ctx *ctx, uint32_t microseconds, rq_stream stream) {
     if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device) != hipSuccess || khz <= 0) khz = 100000;
     const uint64_t ticks = (uint64_t)microseconds * (uint64_t)khz / 1000u;
     hipLaunchKernelGGL(k_device_delay, dim3(1), dim3(64), 0, pick(ctx, stream), ticks);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+int rq_device_clock(rq_ctx *ctx, uint64_t *dst, uint64_t *ticks_per_second, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (!dst) return fail(RQ_ERR_INVALID_ARGUMENT, "null destination");
+    if (ticks_per_second) {
+        int khz = 0;
+        RQ_HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device));
+        if (khz <= 0) return fail(RQ_ERR_HIP, "device reports no wall clock rate");
+        *ticks_per_second = (uint64_t)khz * 1000u;
+    }
+    hipLaunchKernelGGL(k_device_clock, dim3(1), dim3(64), 0, pick(ctx, stream), dst);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+int rq_stream_probe(rq_ctx *ctx, const void *src, size_t row_bytes, size_t rows, int rows_per_block, void *dst,
+                    int store, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (rows == 0) return RQ_OK;
+    if (!src || !dst) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (row_bytes == 0 || row_bytes % 16 != 0 || row_bytes > 16384)
+        return fail(RQ_ERR_SHAPE, "row_bytes must be a multiple of 16 in 16..16384");
+    if (rows_per_block < 1 || rows_per_block > 4) return fail(RQ_ERR_SHAPE, "rows_per_block must be 1..4");
+    if (rows > 0x7fffffff || rows * row_bytes > 0xffffffffull) return fail(RQ_ERR_SHAPE, "too many rows");
+    if (!aligned(src, 16) || !aligned(dst, 2)) return fail(RQ_ERR_INVALID_ARGUMENT, "misaligned pointer");
+    const unsigned blocks = (unsigned)cdiv((int64_t)rows, rows_per_block);
+    const int cpt = (int)cdiv((int64_t)row_bytes / 16, 256);
+    const auto *sp = static_cast<const uint8_t *>(src);
+    auto *dp = static_cast<uint16_t *>(dst);
+    hipStream_t s = pick(ctx, stream);
+    const int st = store ? 1 : 0;
+    if (rows_per_block == 1) launch_probe<1>(cpt, blocks, s, sp, (int)row_bytes, (int)rows, dp, st);
+    else if (rows_per_block == 2) launch_probe<2>(cpt, blocks, s, sp, (int)row_bytes, (int)rows, dp, st);
+    else if (rows_per_block == 3) launch_probe<3>(cpt, blocks, s, sp, (int)row_bytes, (int)rows, dp, st);
+    else launch_probe<4>(cpt, blocks, s, sp, (int)row_bytes, (int)rows, dp, st);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }

@@ -1,5 +1,7 @@
-"""rq_device_delay: the bounded device-side wait that benchmark drivers put in
-front of a batch of direct launches (no reference counterpart)."""
+"""Measurement aids and memory plumbing of the C ABI: rq_device_delay (the
+bounded device-side wait that benchmark drivers put in front of a batch of
+direct launches) and rq_stream_probe (the GEMV's weight stream alone), neither
+with a reference counterpart, and rq_memset."""
 import pytest
 
 from rusty_amd import _lib
@@ -114,3 +116,75 @@ def test_swiglu_graph_replays(ctx, engine):
             ctx.sync()
             truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32))
             assert f16_tol_check(Y.to_vec(), truth)[2], f"m={m} replay {rep}"
+
+
+# rq_stream_probe: the GEMV's weight stream without arithmetic (a measurement
+# aid, no reference counterpart).  Wave w of block b XOR-combines the 16-byte
+# chunks its 64 lanes loaded (chunks 64w .. 64w + 63, + 256 j) over the
+# block's rows; with store, lane 0 writes it, folded to 16 bits, for row b*R + w.
+
+def _probe_expect(src, row_bytes, rows, R):
+    import numpy as np
+
+    words = src.view(np.uint32).reshape(rows, row_bytes // 4)
+    out = np.zeros(rows, np.uint16)
+    C = row_bytes // 16
+    for b in range(-(-rows // R)):
+        here = min(R, rows - b * R)
+        for w in range(here):
+            chunks = [c for c0 in range(64 * w, C, 256) for c in range(c0, min(c0 + 64, C))]
+            acc = 0
+            for r in range(here):
+                for c in chunks:
+                    for v in words[b * R + r, 4 * c:4 * c + 4]:
+                        acc ^= int(v)
+            out[b * R + w] = (acc ^ (acc >> 16)) & 0xFFFF
+    return out
+
+
+@pytest.mark.parametrize("row_bytes,rows,R", [(4096, 10, 4), (8192, 7, 2), (16384, 3, 1), (2048, 5, 3)])
+def test_stream_probe_store(ctx, row_bytes, rows, R):
+    import numpy as np
+
+    from rusty_amd import DType, UnifiedTensor
+
+    src = np.random.default_rng(row_bytes + rows).integers(0, 256, rows * row_bytes, dtype=np.uint8)
+    s = UnifiedTensor.new(ctx, src, dtype=DType.U8)
+    d = UnifiedTensor.new(ctx, np.full(rows + 8, 0xDEAD, np.uint16).view(np.uint8), dtype=DType.U8)
+    # store == 0: the loads are consumed, nothing is written
+    _lib.call("rq_stream_probe", ctx.handle, s.ptr, row_bytes, rows, R, d.ptr, 0, None)
+    assert np.all(d.to_vec().view(np.uint16) == 0xDEAD)
+    _lib.call("rq_stream_probe", ctx.handle, s.ptr, row_bytes, rows, R, d.ptr, 1, None)
+    got = d.to_vec().view(np.uint16)
+    np.testing.assert_array_equal(got[:rows], _probe_expect(src, row_bytes, rows, R))
+    assert np.all(got[rows:] == 0xDEAD)  # nothing past the rows
+
+
+def test_stream_probe_limits(ctx):
+    lib = _lib.lib()
+    assert lib.rq_stream_probe(ctx.handle, None, 16, 1, 1, 16, 1, None) == _lib.RQ_ERR_INVALID_ARGUMENT
+    assert lib.rq_stream_probe(ctx.handle, 16, 16, 1, 1, None, 1, None) == _lib.RQ_ERR_INVALID_ARGUMENT
+    assert lib.rq_stream_probe(ctx.handle, 16, 24, 1, 1, 16, 1, None) == _lib.RQ_ERR_SHAPE
+    assert lib.rq_stream_probe(ctx.handle, 16, 16, 1, 5, 16, 1, None) == _lib.RQ_ERR_SHAPE
+    assert lib.rq_stream_probe(ctx.handle, 16, 16384 + 16, 1, 1, 16, 1, None) == _lib.RQ_ERR_SHAPE
+
+
+# rq_device_clock: device wall-clock stamps on the stream (graph-capturable)
+
+def test_device_clock_brackets_a_delay(ctx):
+    import ctypes
+
+    import numpy as np
+
+    from rusty_amd import DType, UnifiedTensor
+
+    buf = UnifiedTensor.new(ctx, np.zeros(16, np.uint8), dtype=DType.U8)
+    hz = ctypes.c_uint64()
+    _lib.call("rq_device_clock", ctx.handle, buf.ptr, ctypes.byref(hz), None)
+    _lib.call("rq_device_delay", ctx.handle, 3000, None)
+    _lib.call("rq_device_clock", ctx.handle, buf.ptr + 8, None, None)
+    t = buf.to_vec().view(np.uint64)
+    ms = (int(t[1]) - int(t[0])) / hz.value * 1e3
+    assert 1e6 <= hz.value <= 1e10
+    assert 2.9 <= ms <= 50.0, ms
+    assert _lib.lib().rq_device_clock(ctx.handle, None, None, None) == _lib.RQ_ERR_INVALID_ARGUMENT
