@@ -180,7 +180,9 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * context's own stream (stream NULL) a GEMM with few tokens splits K over
  * more blocks using the context's workspace, so two such calls of one
  * context must not run concurrently (they cannot on one stream); on any
- * other stream it does not split. */
+ * other stream it does not split.  A HIP graph captured on the context's
+ * stream that holds such GEMMs has the workspace baked in: replay it on the
+ * context's stream (or never concurrently with other work of the context). */
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y,
                rq_dtype y_dtype, int64_t m, rq_stream stream);
 

@@ -346,6 +346,26 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     // arrives last clears the counter for the next launch and adds all the
     // splits' partials in split order (deterministic whichever block is last)
     // before the epilogue.  No block waits for another.
+    //
+    // Ordering.  The counter is a relaxed agent-scope atomic; what orders the
+    // partials around it is the gfx9.4+ memory model itself (the one LLVM's
+    // AMDGPU backend implements for agent scope on multi-XCD parts):
+    //  * an sc1 store is an agent-scope store: it writes through this XCD's
+    //    L2, and its vmcnt decrement is the acknowledgement that it is visible
+    //    at agent scope.  `s_waitcnt vmcnt(0)` (an asm statement with a memory
+    //    clobber, so the compiler keeps every store above it) then the barrier
+    //    make every thread's pieces visible before thread 0 issues the atomic;
+    //  * the atomic executes at the memory side (agent scope), after those
+    //    acknowledged stores;
+    //  * the last block's partial loads are sc1 (agent-scope) loads: they miss
+    //    this XCD's possibly stale L2 lines and read the coherent values.  They
+    //    are issued only after thread 0's atomic has returned (its result is
+    //    what `last` is computed from, published through LDS across a barrier,
+    //    which also keeps the compiler from hoisting them).
+    // An agent-scope release/acquire pair on the counter would add an L2
+    // write-back (buffer_wbl2) and invalidate per block, which the sc1 stores
+    // and loads make unnecessary: with the stores and loads themselves at agent
+    // scope there are no other writes to publish and no stale lines to read.
     if constexpr (BM == 64 && BN == 64) {  // only the 64x64 grids split (see launch_tiled)
         if (splits > 1) {
             constexpr int FNO = FN / KG;  // feature tiles this wave finishes

@@ -77,3 +77,15 @@ def test_c_client_runs(tmp_path):
     r = subprocess.run([str(_build_c_example(tmp_path))], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0 and "abi_example: OK" in r.stdout
+
+
+def test_integration_binding_lists_every_entry_point():
+    """INTEGRATION.md's Rust `extern "C"` block declares exactly the header's functions."""
+    import re
+    from pathlib import Path
+
+    text = (Path(__file__).resolve().parent.parent / "INTEGRATION.md").read_text()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    bound = set(re.findall(r"pub fn (rq_[a-z0-9_]+)\s*\(", block))
+    assert bound == set(_lib.header_symbols()), bound ^ set(_lib.header_symbols())

@@ -60,9 +60,10 @@ def run_collect(runner, prompt, steps):
                 max_seq=600),
 ], ids=["gqa2_hd64", "mqa_hd128", "mha_long", "gqa2_hd128_long", "gqa2_hd128_600"])
 def test_small_models_match_oracle(ctx, cfg):
-    # the runner splits each head's attention over 1 (max_seq <= 160), 2 (<= 320) or 4 blocks:
-    # these models cover 1 and 2 at head_dim 64, 1 and 4 at head_dim 128 (the 1.1B test: 4 at 64);
-    # the 600-position model's splits reach 150 positions, more than one 128-row pass at head_dim 128
+    # the runner splits each head's attention over 1 (max_seq <= 160), 2 (<= 320), 4 (<= 480) or 8
+    # blocks: these models cover 1 and 2 at head_dim 64, 1 and 4 and 8 at head_dim 128 (the 1.1B test:
+    # 8 at 64); a pass covers 128 rows at head_dim 128 and 256 at 64, and no split here exceeds one
+    # pass -- test_attention_multi_pass covers that
     w = synth_weights(cfg, seed=cfg.hidden + cfg.vocab)
     g = np.random.default_rng(11)
     n_prompt = min(40, cfg.max_seq // 2) if cfg.max_seq < 200 else 280
@@ -141,3 +142,84 @@ def test_llama_1b_128_greedy_steps(ctx):
         worst = max(worst, d)
         assert d <= tol, f"step {i}: logits rel diff {d:.3e}"
     print(f"[1B] 128 greedy tokens consistent; logits rel diff (first, last) <= {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("cfg,n_prompt", [
+    (LlamaConfig(n_layers=1, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=256, vocab=300,
+                 max_seq=1100), 1030),
+    (LlamaConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=256, vocab=300,
+                 max_seq=2200), 2060),
+], ids=["hd128_1100", "hd64_2200"])
+def test_attention_multi_pass(ctx, cfg, n_prompt):
+    """Caches long enough that each of the 8 splits per head spans more than one
+    pass of the attention kernel (128 rows at head_dim 128: 129-138 rows per
+    split here; 256 rows at head_dim 64: 258-275): the later passes' loads, the
+    online-softmax rescale and the pass-end barriers, against the f64 oracle."""
+    w = synth_weights(cfg, seed=cfg.max_seq)
+    prompt = np.random.default_rng(cfg.max_seq).integers(0, cfg.vocab, n_prompt)
+    steps = cfg.max_seq - n_prompt
+    r = LlamaRunner(ctx, cfg, w)
+    toks, logits = run_collect(r, prompt, steps)
+    r.close()
+    np.testing.assert_array_equal(toks[:n_prompt], prompt)
+    check_steps(cfg, w, toks, logits, n_prompt, 1e-2, f"multi-pass {cfg.head_dim}x{cfg.max_seq}")
+
+
+def _tie_model():
+    """TINY with the final norm zeroed except element 0 (so the normalised row is
+    xn0 at element 0 and exactly 0 elsewhere) and an lm_head whose row r has code
+    q0 = +127 or -127 at k = 0 (0 elsewhere) and scale s_r: logit_r is exactly
+    q0 * s_r * xn0 as the GEMV computes it, equal for rows with equal (q0, s_r)."""
+    w = synth_weights(TINY, seed=31)
+    fn = np.zeros(TINY.hidden, np.float16)
+    fn[0] = 1.0
+    w.final_norm = fn
+    q = np.zeros((TINY.vocab, TINY.hidden), np.int8)
+    s = np.zeros(TINY.vocab, np.float32)
+    return w, q, s
+
+
+def _pick(ctx, w, n_prompt=5):
+    r = LlamaRunner(ctx, TINY, w)
+    r.prefill(np.arange(1, n_prompt + 1))
+    logits = r.logits()
+    tok = int(r.tokens()[n_prompt])
+    r.close()
+    return tok, logits
+
+
+def test_greedy_pick_ties_and_threshold(ctx):
+    """top_k with k = 1 as the reference scans (kernels.wgsl:173-188): the first
+    index among equal maxima, and index 0 when no logit exceeds -1e9."""
+    # sign of xn0 for these weights: one row with q0 = +127
+    w, q, s = _tie_model()
+    q[0, 0], s[0] = 127, 1.0
+    w.lm_head = (q, s)
+    _, lg = _pick(ctx, w)
+    sgn = 1.0 if lg[0] > 0 else -1.0
+    assert lg[0] != 0.0
+
+    # exact ties: rows 300, 640 and 941 hold the largest logit (positive), rows 200
+    # and 900 the same magnitude negated; every other row 0.  First index wins: 300.
+    w, q, s = _tie_model()
+    for r_ in (300, 640, 941):
+        q[r_, 0], s[r_] = int(127 * sgn), 1e6
+    for r_ in (200, 900):
+        q[r_, 0], s[r_] = int(-127 * sgn), 1e6
+    w.lm_head = (q, s)
+    tok, lg = _pick(ctx, w)
+    assert lg[300] > 0 and lg[300] == lg[640] == lg[941], (lg[300], lg[640], lg[941])
+    assert tok == 300, tok
+    assert tok == ol.greedy(lg.astype(np.float64))
+
+    # nothing above -1e9: every logit is very negative, rows >= 100 less so than
+    # rows < 100 (the largest is at 100), but all are <= -1e9, so the pick is 0
+    w, q, s = _tie_model()
+    q[:, 0] = int(-127 * sgn)
+    s[:] = 1e12
+    s[:100] = 2e12
+    w.lm_head = (q, s)
+    tok, lg = _pick(ctx, w)
+    assert lg.max() <= -1e9 and lg.argmax() == 100, (lg.max(), lg.argmax())
+    assert tok == 0, tok
+    assert tok == ol.greedy(lg.astype(np.float64))
