@@ -28,14 +28,31 @@
 //    bytes) and is expanded to fp16 when a wave reads its fragment:
 //    XOR 0x80 -> q+128, v_perm_b32 under exponent 0x64 -> fp16 1152+q,
 //    v_pk_add_f16 -1152 -> q (exact).
+//  * What staging costs is the cache lines each DMA touches, not its bytes:
+//    one 1 KiB unit of X covers 8 rows x 128 B (8 whole lines); a unit of W
+//    at 64 k per step covered 16 rows x 64 B (16 half lines), and W staging
+//    measured 2x X's cost per unit.  So the large tiles (W2) stage W two
+//    k-steps at a time: 128 B of each row, whole lines, into a ring of two
+//    pairs beside the X ring (the same LDS as four single steps), every other
+//    iteration.  A lane then reads its W fragment as one 16-byte piece that
+//    covers both of its k16 slices (a k permutation matched by the X reads),
+//    so every fragment read is a conflict-free ds_read_b128 (W reads were
+//    ds_read_b64 with a 2-way bank conflict).  256x128: 66.0 -> 64.5 us.
+//  * Measured with the same instruction stream and zero activations, the
+//    kernel runs 27 % faster (61.7 -> 45.1 us at 2048x4096x4096; zero
+//    weights 48.2): with random fp16 data the chip's power limit, not the
+//    schedule, sets the clock.  Deeper rings (6 X stages, or 3 W pairs) and
+//    64x128 wave tiles (less LDS, twice the int8 expansion) measured equal or
+//    slower.
 //  * An S-stage LDS ring, one barrier per k-step.  The loads of a stage are
 //    waited for with an explicit vmcnt (loads retire in order), so the DMA of
 //    the next steps stays in flight.  PINGPONG: the fragments of step k+1 are
 //    read into registers while the MFMAs of step k run.
 //  * LDS layouts are XOR-swizzled per 16-byte chunk (the DMA writes 1 KiB
-//    contiguous per wave, so padding is impossible): X rows (128 B) put chunk
-//    c at c ^ ((row >> 1) & 7), W rows (64 B) at c ^ ((row >> 2) & 3), which
-//    spreads the 32 rows an MFMA operand reads over the banks.
+//    contiguous per wave, so padding is impossible): X rows and W-pair rows
+//    (128 B) put chunk c at c ^ ((row >> 1) & 7), single-step W rows (64 B) at
+//    c ^ ((row >> 2) & 3), which spreads the 32 rows an MFMA operand reads
+//    over the banks.
 //  * Rows past M/N and k past K are offsets past the buffer resource and read
 //    as zero: no branches around the loads; the k loop is padded to the ring
 //    period with zero steps.
@@ -108,13 +125,6 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
     return __builtin_bit_cast(half8, r);
 }
 
-// One ring stage: X tile (BM rows x 64 fp16) and W tile (BN rows x 64 int8).
-template <int BM, int BN>
-struct Stage {
-    uint8_t x[BM * 128];
-    uint8_t w[BN * 64];
-};
-
 // Tile order: consecutive blocks go round-robin to the 8 XCDs, so block b
 // runs on XCD b % 8; it takes position L = (b % 8) * (tiles / 8) + b / 8 of
 // a group-M order (GM m-tiles per group, n-tiles across, m fastest within a
@@ -131,7 +141,7 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
     tn = r / gsize;
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
@@ -145,12 +155,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     constexpr int WGM = WPG / WGN; // wave grid: WGM along tokens, WGN along features
     constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
     static_assert(KG == 1 || (KG == 2 && FN % 2 == 0), "two k-groups split the finishing work by feature tiles");
-    constexpr int XUW = BM * 128 / 1024 / NW, WUW = BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
+    // W2: the weight is staged two k-steps at a time (128-byte row pieces, whole
+    // cache lines) in a ring of two pairs beside an S-stage X ring.
+    static_assert(!W2 || (KG == 2 && PINGPONG && S == 4), "W pairs: two k-groups, ping-pong, 4 X stages");
+    constexpr int XUW = BM * 128 / 1024 / NW;
+    constexpr int WUW = W2 ? BN * 128 / 1024 / NW : BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
     static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
-    static_assert(S >= 3 && S * (BM * 128 + BN * 64) <= 160 * 1024, "ring does not fit in LDS");
-    constexpr int NOUT = XUW + WUW;  // DMA ops per wave per k-step
+    constexpr int XSTRIDE = W2 ? BM * 128 : BM * 128 + BN * 64;  // bytes between X stages
+    constexpr int RING_K = W2 ? S * BM * 128 + 2 * BN * 128 : S * (BM * 128 + BN * 64);  // k-loop stages
+    // the epilogue reuses the ring to stage a tile of f32 (or fp16) rows
+    constexpr int RING = RING_K > BM * (BN * 4 + 16) ? RING_K : BM * (BN * 4 + 16);
+    static_assert(S >= 3 && RING <= 160 * 1024, "ring does not fit in LDS");
+    constexpr int NOUT = XUW + WUW;  // DMA ops per wave per k-step (W2: W on odd steps only)
 
-    __shared__ __attribute__((aligned(1024))) Stage<BM, BN> ring[S];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[RING];
 
     // Split-K (splits > 1): block b multiplies tile b % tiles over the split
     // b / tiles of its k-steps; the tile's last block to finish adds every
@@ -181,8 +199,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     }
 #pragma unroll
     for (int q = 0; q < WUW; ++q) {
-        const int row = (wave * WUW + q) * 16 + lane / 4, s = lane % 4;
-        woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 2) & 3)) * 16;
+        if constexpr (W2) {
+            // 8 rows x 128 bytes (two k-steps) per unit, chunk s of row r holding
+            // global chunk s ^ ((r >> 1) & 7)
+            const int row = (wave * WUW + q) * 8 + lane / 8, s = lane % 8;
+            woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 1) & 7)) * 16;
+        } else {
+            const int row = (wave * WUW + q) * 16 + lane / 4, s = lane % 4;
+            woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 2) & 3)) * 16;
+        }
     }
     // LDS address of the ring, taken once: per-stage addresses are then plain
     // scalar sums (a generic-to-LDS pointer cast in the loop costs a null check
@@ -191,10 +216,22 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     auto dma = [&](int stage, int kt) {
         const bool live = kt < nk;
         kt += k0;
-        const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)sizeof(Stage<BM, BN>);
-        const uint32_t sw = sx + (uint32_t)(BM * 128);  // the W tile follows the X tile
+        const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)XSTRIDE;
 #pragma unroll
         for (int q = 0; q < XUW; ++q) dma16(rx, sx + (uint32_t)(wave * XUW + q) * 1024u, live ? xoff[q] + kt * 128 : kOOB);
+        if constexpr (!W2) {
+            const uint32_t sw = sx + (uint32_t)(BM * 128);  // the W tile follows the X tile
+#pragma unroll
+            for (int q = 0; q < WUW; ++q) dma16(rw, sw + (uint32_t)(wave * WUW + q) * 1024u, live ? woff[q] + kt * 64 : kOOB);
+        }
+    };
+    // W2: the weight of steps kt, kt + 1 (kt even) into pair slot `pair`.  The
+    // second step past this block's k range reads the next bytes of the row
+    // (or zeros past the weight): finite codes that only meet zero activations.
+    auto dma_w = [&](int pair, int kt) {
+        const bool live = kt < nk;
+        kt += k0;
+        const uint32_t sw = ring_lds + (uint32_t)(S * BM * 128) + (uint32_t)pair * (uint32_t)(BN * 128);
 #pragma unroll
         for (int q = 0; q < WUW; ++q) dma16(rw, sw + (uint32_t)(wave * WUW + q) * 1024u, live ? woff[q] + kt * 64 : kOOB);
     };
@@ -208,23 +245,47 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // A k-step's fragments: raw int8 W (expanded just before the MFMA) and fp16 X.
+    // W2 reads a lane's W as one 16-byte piece covering both of its k16 slices
+    // (a k permutation: slice kl takes bytes 8 kl .. 8 kl + 7 of the piece at
+    // k = 32 kg + 16 h, and X supplies the same k), so every fragment read is a
+    // conflict-free ds_read_b128.
     struct Frag {
         uint2 w[K16][FN];
         half8 x[K16][FM];
     };
-    auto fetch = [&](const Stage<BM, BN> &st, Frag &f) {
-#pragma unroll
-        for (int kl = 0; kl < K16; ++kl) {
-            const int k16 = kg * K16 + kl;
+    auto fetch = [&](int stage, int kt, Frag &f) {
+        const uint8_t *sx = ring + stage * XSTRIDE;
+        if constexpr (W2) {
+            const uint8_t *sw = ring + S * BM * 128 + ((kt >> 1) & 1) * (BN * 128);
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
-                const int r = wn * TN + i * 32 + fr;
-                f.w[kl][i] = *reinterpret_cast<const uint2 *>(st.w + r * 64 + ((k16 ^ ((r >> 2) & 3)) * 16) + h * 8);
+                const int r = wn * TN + i * 32 + fr, c = (kt & 1) * 4 + 2 * kg + h;
+                const uint4 v = *reinterpret_cast<const uint4 *>(sw + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+                f.w[0][i] = make_uint2(v.x, v.y);
+                f.w[1][i] = make_uint2(v.z, v.w);
             }
 #pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const int r = wm * TM + j * 32 + fr, c = 2 * k16 + h;
-                f.x[kl][j] = *reinterpret_cast<const half8 *>(st.x + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+            for (int kl = 0; kl < K16; ++kl)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int r = wm * TM + j * 32 + fr, c = 4 * kg + 2 * h + kl;
+                    f.x[kl][j] = *reinterpret_cast<const half8 *>(sx + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+                }
+        } else {
+            const uint8_t *sw = sx + BM * 128;
+#pragma unroll
+            for (int kl = 0; kl < K16; ++kl) {
+                const int k16 = kg * K16 + kl;
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    const int r = wn * TN + i * 32 + fr;
+                    f.w[kl][i] = *reinterpret_cast<const uint2 *>(sw + r * 64 + ((k16 ^ ((r >> 2) & 3)) * 16) + h * 8);
+                }
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int r = wm * TM + j * 32 + fr, c = 2 * k16 + h;
+                    f.x[kl][j] = *reinterpret_cast<const half8 *>(sx + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+                }
             }
         }
     };
@@ -252,7 +313,43 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     using Ls2 = std::integral_constant<int, S - 2>;
     using Ls1 = std::integral_constant<int, S - 1>;
 
-    if constexpr (PINGPONG) {
+    if constexpr (W2) {
+        // Iteration u (step kt = base + u): wait until step kt+1 has landed,
+        // read its fragments while the MFMAs of kt run, then refill: odd
+        // iterations first load the W pair (kt+3, kt+4) into the slot of the
+        // pair (kt-1, kt), whose last fragments were read before this
+        // iteration's barrier; every iteration loads X of step kt+4 into the
+        // X stage of kt.  vmcnt counts (loads retire in order): an even
+        // iteration needs everything through iteration u-3 (its W pair was the
+        // first load there), so iterations u-2 (X) and u-1 (W, X) may stay in
+        // flight; an odd one needs the W pair of iteration u-2, so that
+        // iteration's X and iteration u-1's X may.  The prologue issues steps
+        // 0-3 as iterations -4..-1 would have.
+        constexpr int WAIT_EVEN = 2 * XUW + WUW, WAIT_ODD = 2 * XUW;
+        Frag f[2];
+        dma(0, 0);
+        dma_w(0, 0);
+        dma(1, 1);
+        dma(2, 2);
+        dma_w(1, 2);
+        dma(3, 3);
+        wait_vmcnt<3 * XUW + WUW>();
+        __syncthreads();
+        fetch(0, 0, f[0]);
+#pragma unroll 1
+        for (int kt = 0; kt < nk; kt += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (u % 2 == 0) wait_vmcnt<WAIT_EVEN>();
+                else wait_vmcnt<WAIT_ODD>();
+                __syncthreads();
+                fetch((u + 1) % 4, kt + u + 1, f[(u + 1) % 2]);
+                mma(f[u % 2]);
+                if (u % 2 == 1) dma_w(((kt + u + 3) >> 1) & 1, kt + u + 3);
+                dma(u, kt + u + 4);
+            }
+        }
+    } else if constexpr (PINGPONG) {
         // Step k: step k+1 is ready, step k's stage is free (its fragments are
         // in registers), so DMA(k+S) refills it while the fragments of k+1
         // are read and the MFMAs of k run.
@@ -261,7 +358,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 #pragma unroll
         for (int j = 0; j < S; ++j) dma(j, j);
         ready(Ls1{});
-        fetch(ring[0], f[0]);
+        fetch(0, 0, f[0]);
 #pragma unroll 1
         for (int kt = 0; kt < nk; kt += U) {
 #pragma unroll
@@ -273,12 +370,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
                     // reaching its MFMAs (the ring leaves the DMA S - 1 steps
                     // to land): 1-3 % faster at 256x128 and 128x128, 2 %
                     // slower with one group at 128x64
-                    fetch(ring[(u + 1) % S], f[(u + 1) % 2]);
+                    fetch((u + 1) % S, kt + u + 1, f[(u + 1) % 2]);
                     mma(f[u % 2]);
                     dma(u % S, kt + u + S);
                 } else {
                     dma(u % S, kt + u + S);
-                    fetch(ring[(u + 1) % S], f[(u + 1) % 2]);
+                    fetch((u + 1) % S, kt + u + 1, f[(u + 1) % 2]);
                     mma(f[u % 2]);
                 }
             }
@@ -293,7 +390,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
             for (int u = 0; u < S; ++u) {
                 ready(Ls2{});
                 dma((u + S - 1) % S, kt + u + S - 1);
-                fetch(ring[u % S], f);
+                fetch(u % S, kt + u, f);
                 mma(f);
             }
         }
@@ -306,7 +403,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         // (now idle) ring, lane-contiguous 16-byte pieces, and adds the other
         // group's partials of its own tiles.
         constexpr int HF = FN / 2;  // feature tiles per group
-        static_assert(2 * WPG * HF * FM * 16 * 64 * 4 <= S * (int)sizeof(Stage<BM, BN>), "exchange does not fit");
+        static_assert(2 * WPG * HF * FM * 16 * 64 * 4 <= RING, "exchange does not fit");
         float4 *xch = reinterpret_cast<float4 *>(&ring[0]);
         // slot of (target group, wave position, tile pair (i / 2, j), quad r4), then lane
         auto slot = [&](int tg, int ih, int j, int r4) { return (((tg * WPG + wq) * HF + ih) * FM + j) * 4 + r4; };
@@ -459,7 +556,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         auto staged = [&](auto eb_c) {
             constexpr int EB = decltype(eb_c)::value;  // output element bytes
             constexpr int RS = BN * EB + 16;           // padded LDS row stride
-            static_assert(BM * RS <= S * (int)sizeof(Stage<BM, BN>), "output staging does not fit in the ring");
+            static_assert(BM * RS <= RING, "output staging does not fit in the ring");
             uint8_t *ot = reinterpret_cast<uint8_t *>(&ring[0]);
             __syncthreads();  // every wave is done with the ring (and the k-group exchange)
 #pragma unroll
@@ -556,7 +653,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 // N = 11008: 19.0 -> 17.7 (2).  Only on the context's own stream (ws.partials
 // is null otherwise); the larger tiles gained nothing from splitting (their
 // LDS rings allow one block per CU).
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1>
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false>
 int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, int64_t cus,
                  const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
@@ -570,7 +667,7 @@ int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64
         while (splits > 1 && (size_t)(tiles * splits) * BM * BN > ws.floats) --splits;
         splits = cdiv(nk, cdiv(nk, splits));  // every split gets k-steps (the kernel's ks = ceil(nk / splits))
     }
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG>), dim3((unsigned)(tiles * splits)),
+    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2>), dim3((unsigned)(tiles * splits)),
                        dim3(64 * NW), 0, s, (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y,
                        yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm, (int)splits,
                        ws.partials, ws.counters);
@@ -598,14 +695,19 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // 61.2 us (128x128: 76.3); N = 11008, m = 256: 128x128 39.1 (64x64: 41.1).
     // Groups of 4 token panels per XCD and the ping-pong fragments beat
     // token-major order and single buffering by 5-15 % at m = 2048.  The two
-    // large tiles run two k-groups of 4 waves; at 128x64 and 64x64 one group
-    // of 4 waves measured 2-4 % faster.
+    // large tiles run two k-groups of 4 waves with the weight staged in pairs
+    // of k-steps; at 128x64 and 64x64 one group of 4 waves measured 2-4 %
+    // faster.  128x256 rather than 256x128: for the same outputs per block
+    // (one 128x64 wave tile per wave) it stages 32 KiB per k-step instead of
+    // 40, in 256 cache lines instead of 320 (2048x4096x4096 64.5 -> 62.1 us,
+    // N = 11008 176.4 -> 171.2, K = 11008 162.5 -> 156.9 us in one run), and
+    // it fills the device whenever 256x128 would.
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     // a tile taller than the tokens (rounded up to 64) only multiplies padding:
     // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
     auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (fills(256, 128)) return launch_tiled<256, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2>(w, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 256)) return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, x, y, yt, m, 4, cus, ws, s);
     if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
     return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
 }

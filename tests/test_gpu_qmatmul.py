@@ -187,8 +187,9 @@ def test_config4_prefill(ctx, engine, n, k):
 
 
 # tile per shape on a 256-CU device: 64x64 for the first, second and fourth, 128x64 for
-# (300, 4096), 128x128 (two k-groups of 4 waves) for (770, 4096) and (1100, 4100), 256x128
-# (two k-groups) for (1500, 4100); k = 1088 is 17 k-steps, not a multiple of the LDS ring period
+# (300, 4096), 128x128 (two k-groups of 4 waves, weight staged in pairs of k-steps) for
+# (770, 4096) and (1100, 4100), 128x256 (the same) for (1500, 4100); k = 1088 is 17 k-steps, not a
+# multiple of the LDS ring period, and odd (the last weight pair is half past the k range)
 @pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 136, 2048), (300, 4096, 64), (129, 129, 128),
                                    (770, 4096, 128), (1500, 4100, 64), (1100, 4100, 1088), (1500, 4100, 1088)])
 def test_gemm_ragged(ctx, engine, m, n, k):
