@@ -274,13 +274,22 @@ def _replays(ctx, fn, launches: int, use_graph: bool, reps: int = 3) -> list:
 
 
 def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5,
-            use_graph: bool = True):
+            use_graph: bool = True, operands: str = "random"):
+    """configs[3] dequant-GEMM.  `operands` other than "random" (the benchmark
+    data) zero the activations or the weight codes: the same kernel and
+    instruction stream on data that switches fewer bits, to show how much of
+    the time is the chip's power limit (a diagnostic, never the headline)."""
     from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
 
     g = synth.rng(n + k)
     q, s = synth.rowwise_weight(g, n, k)
+    xa = synth.activations(g, m, k, sigma=0.5)
+    if operands == "zero-activations":
+        xa = np.zeros_like(xa)
+    elif operands == "zero-weights":
+        q = np.zeros_like(q)
     w = QuantizedTensor.rowwise(ctx, q, s)
-    x = UnifiedTensor.new(ctx, synth.activations(g, m, k, sigma=0.5), dtype=DType.FP16)
+    x = UnifiedTensor.new(ctx, xa, dtype=DType.FP16)
     y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
     # the launches are replayed from a HIP graph: back to back on the device,
     # with no host call in between (a Python call per launch costs ~40 us).
@@ -295,8 +304,11 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
     times = [t / steps for t in times]
     ms = sorted(times)[1]
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    return {"shape": f"{m}x{n}x{k}", "ms": round(ms, 5), "tflops": round(tflops, 2),
-            "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+    out = {"shape": f"{m}x{n}x{k}", "ms": round(ms, 5), "tflops": round(tflops, 2),
+           "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+    if operands != "random":
+        out["operands"] = operands
+    return out
 
 
 def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60, use_graph: bool = True) -> dict:
@@ -435,6 +447,9 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
     ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor"],
                     help="run one extra workload alone, no headline (for profiling runs)")
+    ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
+                    help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
+                         "the power limit; diagnostic only")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps as direct launches instead of one graph per token (for tools that "
                          "do not trace graphs)")
@@ -459,7 +474,8 @@ def main() -> int:
         elif args.only == "floor":
             out["floor"] = floor_probe(ctx, GemvWorkload(ctx, 1, 4096, 4096), args.steps, use_graph=not args.no_graph)
         elif args.only == "prefill":
-            out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph)
+            out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph,
+                                      operands=args.prefill_operands)
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
         elif args.only == "swiglu":
             out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
