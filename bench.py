@@ -19,7 +19,9 @@ Printed JSON (one line, stdout):
                    f32 GEMV on the load-time-dequantized f32 weight (oracle port)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
   prefill_mid      the same GEMM at M=256 and 512 (4096x4096), not a configs[] shape
-  decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2])
+  decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2]), and
+                   the reference's affine format (u8 codes, scale+bias per 64)
+  prefill_affine   the dequant-GEMM on affine weights, fp16 and f32 activations
   swiglu           configs[2]: the fused SwiGLU MLP (gate+up pass, then down)
                    at the 7B shape, M=1 and M=8, GB/s of its algorithmic bytes
   decode_tok_s     configs[4]: 1.1B int8 Llama, 512-token prompt, then 128
@@ -53,30 +55,42 @@ def gemv_bytes(m: int, n: int, k: int) -> int:
 
 
 class GemvWorkload:
-    """COPIES rotating per-row int8 weights [n, k] plus X [m, k], Y [m, n] fp16."""
+    """COPIES rotating int8 weights [n, k] plus X [m, k], Y [m, n] fp16.  Per-row
+    codes with one f32 scale per row (the configs), or with `affine` the
+    reference's format: u8 codes with an f32 scale and bias per 64 elements."""
 
-    def __init__(self, ctx, m: int, n: int, k: int, seed: int = 0, copies: int = COPIES):
+    def __init__(self, ctx, m: int, n: int, k: int, seed: int = 0, copies: int = COPIES, affine: bool = False):
         from rusty_amd import DType, UnifiedTensor, _lib, synth
 
         self.ctx, self.m, self.n, self.k, self.copies = ctx, m, n, k, copies
         g = synth.rng(seed)
-        q, s = synth.rowwise_weight(g, n, k)
+        if affine:
+            q, s, b = synth.affine_weight(g, n, k, 64)
+        else:
+            (q, s), b = synth.rowwise_weight(g, n, k), None
         x = synth.activations(g, m, k)
-        self.codes = UnifiedTensor.empty(ctx, [copies, n, k], DType.I8)
-        self.scales = UnifiedTensor.empty(ctx, [copies, n], DType.FP32)
-        first = UnifiedTensor.new(ctx, q, dtype=DType.I8)
+        ns = s.size  # scales (and biases) per copy
+        self.codes = UnifiedTensor.empty(ctx, [copies, n, k], DType.U8)
+        self.scales = UnifiedTensor.empty(ctx, [copies, ns], DType.FP32)
+        self.biases = UnifiedTensor.empty(ctx, [copies, ns], DType.FP32) if affine else None
+        first = UnifiedTensor.new(ctx, q.view(np.uint8), dtype=DType.U8)
         fs = UnifiedTensor.new(ctx, s)
+        fb = UnifiedTensor.new(ctx, b) if affine else None
         for c in range(copies):
             _lib.call("rq_memcpy_d2d", ctx.handle, self.codes.ptr + c * n * k, first.ptr, n * k, None)
-            _lib.call("rq_memcpy_d2d", ctx.handle, self.scales.ptr + c * n * 4, fs.ptr, n * 4, None)
+            _lib.call("rq_memcpy_d2d", ctx.handle, self.scales.ptr + c * ns * 4, fs.ptr, ns * 4, None)
+            if affine:
+                _lib.call("rq_memcpy_d2d", ctx.handle, self.biases.ptr + c * ns * 4, fb.ptr, ns * 4, None)
         ctx.sync()
         self.x = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
         self.y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
-        self.desc = [_lib.rq_qweight(self.codes.ptr + c * n * k, self.scales.ptr + c * n * 4, None, n, k,
-                                     _lib.RQ_Q_ROWWISE_I8, 0) for c in range(copies)]
+        fmt = _lib.RQ_Q_AFFINE_U8 if affine else _lib.RQ_Q_ROWWISE_I8
+        self.desc = [_lib.rq_qweight(self.codes.ptr + c * n * k, self.scales.ptr + c * ns * 4,
+                                     self.biases.ptr + c * ns * 4 if affine else None, n, k, fmt, 64 if affine else 0)
+                     for c in range(copies)]
         self._fn = _lib.lib().rq_qmatmul
         self._h = ctx.handle
-        self.bytes = gemv_bytes(m, n, k)
+        self.bytes = gemv_bytes(m, n, k) + (4 * n * k // 64 * 2 - 4 * n if affine else 0)
 
     def launch(self, i: int) -> None:
         st = self._fn(self._h, ctypes.byref(self.desc[i % self.copies]), self.x.ptr, 1, self.y.ptr, 1, self.m, None)
@@ -274,22 +288,28 @@ def _replays(ctx, fn, launches: int, use_graph: bool, reps: int = 3) -> list:
 
 
 def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup: int = 5,
-            use_graph: bool = True, operands: str = "random"):
+            use_graph: bool = True, operands: str = "random", affine: bool = False, x_f32: bool = False):
     """configs[3] dequant-GEMM.  `operands` other than "random" (the benchmark
     data) zero the activations or the weight codes: the same kernel and
     instruction stream on data that switches fewer bits, to show how much of
-    the time is the chip's power limit (a diagnostic, never the headline)."""
+    the time is the chip's power limit (a diagnostic, never the headline).
+    `affine`: the reference's weight format (u8 codes, f32 scale and bias per
+    64 elements); `x_f32`: f32 activations (the reference's dtype), cast to
+    fp16 on the device inside the timed call."""
     from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
 
     g = synth.rng(n + k)
-    q, s = synth.rowwise_weight(g, n, k)
-    xa = synth.activations(g, m, k, sigma=0.5)
+    if affine:
+        q, s, b = synth.affine_weight(g, n, k, 64)
+    else:
+        (q, s), b = synth.rowwise_weight(g, n, k), None
+    xa = synth.activations(g, m, k, sigma=0.5, dtype=np.float32 if x_f32 else np.float16)
     if operands == "zero-activations":
         xa = np.zeros_like(xa)
     elif operands == "zero-weights":
         q = np.zeros_like(q)
-    w = QuantizedTensor.rowwise(ctx, q, s)
-    x = UnifiedTensor.new(ctx, xa, dtype=DType.FP16)
+    w = QuantizedTensor.affine(ctx, q, s, b, 64) if affine else QuantizedTensor.rowwise(ctx, q, s)
+    x = UnifiedTensor.new(ctx, xa, dtype=DType.FP32 if x_f32 else DType.FP16)
     y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
     # the launches are replayed from a HIP graph: back to back on the device,
     # with no host call in between (a Python call per launch costs ~40 us).
@@ -308,6 +328,9 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
            "frac_of_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
     if operands != "random":
         out["operands"] = operands
+    if affine or x_f32:
+        out["weights"] = "affine u8, scale+bias per 64" if affine else "per-row int8"
+        out["activations"] = "f32 (cast on device)" if x_f32 else "fp16"
     return out
 
 
@@ -419,16 +442,19 @@ def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
     """configs[1] at M = 4, 16 and the SwiGLU-shaped GEMVs at M = 1, 8, each
     over enough rotating weight copies to stay out of the Infinity Cache."""
     extra = {}
-    for m, n, k in ((4, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 11008, 4096), (1, 4096, 11008),
-                    (8, 4096, 11008)):
+    for m, n, k, aff in ((4, 4096, 4096, False), (16, 4096, 4096, False), (1, 11008, 4096, False),
+                         (8, 11008, 4096, False), (1, 4096, 11008, False), (8, 4096, 11008, False),
+                         (1, 4096, 4096, True), (4, 4096, 4096, True), (16, 4096, 4096, True)):
         copies = max(2, min(COPIES, (1200 << 20) // (n * k)))
-        w2 = GemvWorkload(ctx, m, n, k, copies=copies)
+        w2 = GemvWorkload(ctx, m, n, k, copies=copies, affine=aff)
         wms, _ = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
         kms = wms / (20 * copies)
-        extra[f"m{m}_{n}x{k}"] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1),
-                                  "us_per_launch": round(kms * 1e3, 2),
-                                  "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        log(f"GEMV m={m} {n}x{k}: {extra[f'm{m}_{n}x{k}']}")
+        key = f"m{m}_{n}x{k}" + ("_affine" if aff else "")
+        extra[key] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1), "us_per_launch": round(kms * 1e3, 2),
+                      "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": w2.bytes}
+        if aff:
+            extra[key]["weights"] = "affine u8, f32 scale+bias per 64 (the reference's format)"
+        log(f"GEMV {key}: {extra[key]}")
         del w2
     return extra
 
@@ -536,6 +562,10 @@ def main() -> int:
         # mid-size m (a short prompt, or a batch of decode streams): not a configs[] shape
         result["prefill_mid"] = [prefill(ctx, engine, 4096, 4096, m=m, steps=args.prefill_steps) for m in (256, 512)]
         log(f"prefill (mid-size m) {result['prefill_mid']}")
+        # the reference's own inputs: affine u8 weights (MLX, group 64), fp16 and f32 activations
+        result["prefill_affine"] = [prefill(ctx, engine, 4096, 4096, steps=args.prefill_steps, affine=True, x_f32=f)
+                                    for f in (False, True)]
+        log(f"prefill (affine weights) {result['prefill_affine']}")
         sw = [swiglu(ctx, engine, m) for m in (1, 8)]
         for e in sw:
             log(f"swiglu {e}")

@@ -42,9 +42,16 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Per-file flags.  gemm.hip flushes f32 denormals: that lets the compiler
+# select v_fma_mix{lo,hi}_f16 for the affine weight expansion (fma of an fp16
+# and two f32 operands, rounded once to fp16); the file's only other f32 VALU
+# math is the epilogue's scale multiply of O(1) sums.
+FILE_FLAGS = {"gemm.hip": ["-fgpu-flush-denormals-to-zero"]}
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

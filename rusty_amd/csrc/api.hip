@@ -178,6 +178,7 @@ int rq_ctx_create(int device, rq_ctx **out) {
     ctx->num_cus = prop.multiProcessorCount;
     ctx->sk_partials = nullptr;
     ctx->sk_counters = nullptr;
+    ctx->prep = nullptr;
     // Default priority on purpose: streams of mixed priorities are not used.
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
@@ -199,6 +200,13 @@ int rq_ctx_create(int device, rq_ctx **out) {
         }
         (void)hipGetLastError();  // a failed optional allocation is not the caller's error
     }
+    // Input preparation of the prefill GEMM for affine weights and f32
+    // activations; without it those requests take the generic kernel.
+    {
+        void *p = nullptr;
+        if (hipMalloc(&p, kGemmPrepBytes) == hipSuccess) ctx->prep = p;
+        (void)hipGetLastError();
+    }
     noalloc_init(device);  // the no-alloc SwiGLU's scratch address on this device
     *out = ctx;
     return RQ_OK;
@@ -210,6 +218,7 @@ int rq_ctx_destroy(rq_ctx *ctx) {
     hipError_t e1 = hipStreamSynchronize(ctx->stream);
     hipError_t e2 = hipStreamDestroy(ctx->stream);
     if (ctx->sk_partials) (void)hipFree(ctx->sk_partials);
+    if (ctx->prep) (void)hipFree(ctx->prep);
     delete ctx;
     if (e1 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e1));
     if (e2 != hipSuccess) return fail(RQ_ERR_HIP, "hipStreamDestroy: %s", hipGetErrorString(e2));
@@ -414,8 +423,14 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 }  // extern "C"
 
 rq::GemmWorkspace rq::gemm_workspace(const rq_ctx *ctx, hipStream_t s) {
-    if (!ctx->sk_partials || s != ctx->stream) return GemmWorkspace{nullptr, nullptr, 0, 0};
-    return GemmWorkspace{ctx->sk_partials, ctx->sk_counters, kGemmSkFloats, kGemmSkCounters};
+    GemmWorkspace ws{nullptr, nullptr, 0, 0};
+    if (s != ctx->stream) return ws;
+    if (ctx->sk_partials) ws = GemmWorkspace{ctx->sk_partials, ctx->sk_counters, kGemmSkFloats, kGemmSkCounters};
+    if (ctx->prep) {
+        ws.prep = ctx->prep;
+        ws.prep_bytes = kGemmPrepBytes;
+    }
+    return ws;
 }
 
 // Fused linear dispatch (arguments already validated): decode kernels for

@@ -18,6 +18,9 @@ struct rq_ctx {
     // arrival counters), allocated at create; null if that allocation failed.
     float *sk_partials;
     int *sk_counters;
+    // Staging area of the prefill GEMM's input preparation (affine scales in
+    // [group][row] order, f32 activations cast to fp16), allocated at create.
+    void *prep;
 };
 
 namespace rq {
@@ -79,11 +82,17 @@ int launch_gemv(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
 // kGemmSkCounters per-tile counters (one 128-byte line each, zero between launches).
 constexpr size_t kGemmSkFloats = (size_t)8 << 20;  // 32 MiB
 constexpr int kGemmSkCounters = 4096;
+// Input-preparation area of the prefill GEMM: affine scales transposed to
+// [group][row] (8 bytes per group), then f32 activations cast to fp16 (a
+// chunk of rows at a time when they do not fit).
+constexpr size_t kGemmPrepBytes = (size_t)64 << 20;  // 64 MiB
 struct GemmWorkspace {
     float *partials;  // null: no split-K
     int *counters;
     size_t floats;
     int n_counters;
+    void *prep = nullptr;  // null: no affine or f32-activation GEMM (the generic kernel serves them)
+    size_t prep_bytes = 0;
 };
 // The workspace of ctx when work on stream s may use it: the context's own
 // stream only (two GEMMs running at once on different streams would share it).

@@ -98,6 +98,16 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_add
                  : "memory", "m0");
 }
 
+// DMA of 4 bytes per lane: LDS[lds_addr + 4 * lane] = buffer[voff] (the
+// affine weight's scales of a k-step, see the kernel).
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
 // Waits until at most N vector-memory operations of this wave are outstanding
 // (they retire in issue order).  Inline asm with a memory clobber, so the
 // compiler cannot move LDS reads of the landed data above the wait.
@@ -125,6 +135,25 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
     return __builtin_bit_cast(half8, r);
 }
 
+// 8 unsigned affine codes u (two dwords) -> fp16 u*s + b, given c = b - 1024 s:
+// v_perm_b32 under exponent 0x64 gives fp16 1024 + u exactly, and
+// v_fma_mix{lo,hi}_f16 evaluates fma(1024 + u, s, c) in f32 with one rounding
+// to fp16 (this translation unit flushes f32 denormals, which lets the
+// compiler select the mixed-precision FMA: 1.5 VALU per weight).
+__device__ __forceinline__ uint32_t u8x2_affine(uint32_t u, uint32_t sel, float s, float c) {
+    const h2_t m = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, u, sel));
+    const h2_t r = {(_Float16)__builtin_fmaf((float)m.x, s, c), (_Float16)__builtin_fmaf((float)m.y, s, c)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ half8 u8x8_affine(uint2 w, float s, float c) {
+    uint4 r;
+    r.x = u8x2_affine(w.x, 0x04010400u, s, c);
+    r.y = u8x2_affine(w.x, 0x04030402u, s, c);
+    r.z = u8x2_affine(w.y, 0x04010400u, s, c);
+    r.w = u8x2_affine(w.y, 0x04030402u, s, c);
+    return __builtin_bit_cast(half8, r);
+}
+
 // Tile order: consecutive blocks go round-robin to the 8 XCDs, so block b
 // runs on XCD b % 8; it takes position L = (b % 8) * (tiles / 8) + b / 8 of
 // a group-M order (GM m-tiles per group, n-tiles across, m fastest within a
@@ -141,12 +170,19 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
     tn = r / gsize;
 }
 
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false>
-__global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restrict__ W, const float *__restrict__ scales,
+// FMT 0: per-row int8 codes, scales[n] applied in the epilogue.  FMT 1: the
+// reference's affine u8 codes with a scale and bias per group of G (a multiple
+// of 64) along k; `scales` then holds them transposed, per group g a row of N
+// scales s and a row of N offsets c = b - 1024 s (gemm_affine_prep), so a
+// k-step's values for the block's BN features are contiguous: each wave
+// stages 64 of them per k-step (one 4-byte DMA per lane) beside its X stage,
+// and the weight is expanded to fp16 u*s + b while the fragments are read.
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, int FMT = 0>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm, int splits, float *__restrict__ skw,
-                                                     int *__restrict__ skc) {
+                                                     int *__restrict__ skc, int group) {
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -161,12 +197,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     constexpr int XUW = BM * 128 / 1024 / NW;
     constexpr int WUW = W2 ? BN * 128 / 1024 / NW : BN * 64 / 1024 / NW;  // 1 KiB DMA units per wave
     static_assert(FM >= 1 && FN >= 1 && XUW >= 1 && WUW >= 1, "tile too small");
+    static_assert(FMT == 0 || 2 * BN <= 64 * NW, "affine: one 4-byte DMA per lane covers a k-step's s and c");
     constexpr int XSTRIDE = W2 ? BM * 128 : BM * 128 + BN * 64;  // bytes between X stages
-    constexpr int RING_K = W2 ? S * BM * 128 + 2 * BN * 128 : S * (BM * 128 + BN * 64);  // k-loop stages
+    constexpr int SCB = FMT == 1 ? 64 * NW * 4 : 0;  // affine s and c of one k-step (per X stage)
+    constexpr int RING_X = W2 ? S * BM * 128 + 2 * BN * 128 : S * (BM * 128 + BN * 64);  // X and W stages
+    constexpr int RING_K = RING_X + S * SCB;  // k-loop stages
     // the epilogue reuses the ring to stage a tile of f32 (or fp16) rows
     constexpr int RING = RING_K > BM * (BN * 4 + 16) ? RING_K : BM * (BN * 4 + 16);
     static_assert(S >= 3 && RING <= 160 * 1024, "ring does not fit in LDS");
-    constexpr int NOUT = XUW + WUW;  // DMA ops per wave per k-step (W2: W on odd steps only)
+    constexpr int XOPS = XUW + (FMT == 1 ? 1 : 0);  // DMA ops per wave issued with each X stage
+    constexpr int NOUT = XOPS + WUW;  // DMA ops per wave per k-step (W2: W on odd steps only)
 
     __shared__ __attribute__((aligned(1024))) uint8_t ring[RING];
 
@@ -188,6 +228,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 
     const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
     const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
+    // affine: lane l of wave w stages value i = 64 w + l of [s | c] for the
+    // block's features (rows past N and lanes past 2 BN read zero); the
+    // transposed scales hold 2 N floats per group
+    const int gstep = FMT == 1 ? group / 64 : 1;  // k-steps per scale group
+    const auto rsc = make_rsrc(scales, FMT == 1 ? (uint32_t)(K / group) * (uint32_t)N * 8u : 0u);
+    uint32_t scoff = kOOB;
+    if constexpr (FMT == 1) {
+        const int i = wave * 64 + lane, n = n0 + (i < BN ? i : i - BN);
+        if (i < 2 * BN && n < N) scoff = (uint32_t)((i < BN ? 0 : N) + n) * 4u;
+    }
 
     // Source offsets (k = 0) of this lane in each of the wave's DMA units,
     // swizzled so LDS chunk s of row r holds global chunk s ^ f(r).
@@ -217,6 +267,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         const bool live = kt < nk;
         kt += k0;
         const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)XSTRIDE;
+        if constexpr (FMT == 1)
+            dma4(rsc, ring_lds + (uint32_t)(RING_X + stage * SCB + wave * 256),
+                 live && scoff != kOOB ? scoff + (uint32_t)(kt / gstep) * (uint32_t)N * 8u : kOOB);
 #pragma unroll
         for (int q = 0; q < XUW; ++q) dma16(rx, sx + (uint32_t)(wave * XUW + q) * 1024u, live ? xoff[q] + kt * 128 : kOOB);
         if constexpr (!W2) {
@@ -252,9 +305,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
     struct Frag {
         uint2 w[K16][FN];
         half8 x[K16][FM];
+        float s[FMT == 1 ? FN : 1], c[FMT == 1 ? FN : 1];  // affine: the scale and offset of each W row
     };
     auto fetch = [&](int stage, int kt, Frag &f) {
         const uint8_t *sx = ring + stage * XSTRIDE;
+        if constexpr (FMT == 1) {
+            const float *sc = reinterpret_cast<const float *>(ring + RING_X + stage * SCB);
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int r = wn * TN + i * 32 + fr;
+                f.s[i] = sc[r];
+                f.c[i] = sc[BN + r];
+            }
+        }
         if constexpr (W2) {
             const uint8_t *sw = ring + S * BM * 128 + ((kt >> 1) & 1) * (BN * 128);
 #pragma unroll
@@ -294,7 +357,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         for (int kl = 0; kl < K16; ++kl) {
             half8 a[FN];
 #pragma unroll
-            for (int i = 0; i < FN; ++i) a[i] = i8x8_to_half8(f.w[kl][i]);
+            for (int i = 0; i < FN; ++i) {
+                if constexpr (FMT == 1) a[i] = u8x8_affine(f.w[kl][i], f.s[i], f.c[i]);
+                else a[i] = i8x8_to_half8(f.w[kl][i]);
+            }
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -323,9 +389,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         // iteration needs everything through iteration u-3 (its W pair was the
         // first load there), so iterations u-2 (X) and u-1 (W, X) may stay in
         // flight; an odd one needs the W pair of iteration u-2, so that
-        // iteration's X and iteration u-1's X may.  The prologue issues steps
-        // 0-3 as iterations -4..-1 would have.
-        constexpr int WAIT_EVEN = 2 * XUW + WUW, WAIT_ODD = 2 * XUW;
+        // iteration's X and iteration u-1's X may (the affine scales count
+        // with their X stage).  The prologue issues steps 0-3 as iterations
+        // -4..-1 would have.
+        constexpr int WAIT_EVEN = 2 * XOPS + WUW, WAIT_ODD = 2 * XOPS;
         Frag f[2];
         dma(0, 0);
         dma_w(0, 0);
@@ -333,7 +400,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
         dma(2, 2);
         dma_w(1, 2);
         dma(3, 3);
-        wait_vmcnt<3 * XUW + WUW>();
+        wait_vmcnt<3 * XOPS + WUW>();
         __syncthreads();
         fetch(0, 0, f[0]);
 #pragma unroll 1
@@ -567,7 +634,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
                     const int fl = wn * TN + i * 32 + 8 * g + h * 4;  // feature within the tile
                     float sc[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sc[r] = n0 + fl + r < N ? scales[n0 + fl + r] : 0.0f;
+                    for (int r = 0; r < 4; ++r) sc[r] = n0 + fl + r < N ? (FMT == 0 ? scales[n0 + fl + r] : 1.0f) : 0.0f;
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
                         uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
@@ -612,7 +679,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
             const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;
             float sc[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? scales[nb + r] : 0.0f;
+            for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? (FMT == 0 ? scales[nb + r] : 1.0f) : 0.0f;
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int mm = m0 + wm * TM + j * 32 + fr;
@@ -654,8 +721,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const int8_t *__restri
 // is null otherwise); the larger tiles gained nothing from splitting (their
 // LDS rings allow one block per CU).
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false>
-int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64_t m, int gm, int64_t cus,
-                 const GemmWorkspace &ws, hipStream_t s) {
+int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
+                 int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
@@ -667,26 +734,57 @@ int launch_tiled(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int64
         while (splits > 1 && (size_t)(tiles * splits) * BM * BN > ws.floats) --splits;
         splits = cdiv(nk, cdiv(nk, splits));  // every split gets k-steps (the kernel's ks = ceil(nk / splits))
     }
-    hipLaunchKernelGGL((k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2>), dim3((unsigned)(tiles * splits)),
-                       dim3(64 * NW), 0, s, (const int8_t *)w.codes, w.scales, (const _Float16 *)x, y,
-                       yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m, tiles_n, gm < 1 ? 1 : gm, (int)splits,
-                       ws.partials, ws.counters);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * splits)), dim3(64 * NW), 0, s, (const uint8_t *)w.codes,
+                           scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m,
+                           tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64);
+    };
+    if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
+    else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0>);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 
-}  // namespace
+// Input preparation (stream-ordered before the GEMM it feeds).
+// Affine scales: out[g][0][n] = s[n][g], out[g][1][n] = b[n][g] - 1024 s[n][g]
+// (gpr = groups per row; b NULL reads as 0), through 64 x 64 LDS tiles so
+// both the reads along g and the writes along n are coalesced.
+__global__ __launch_bounds__(256) void k_affine_prep(const float *__restrict__ s, const float *__restrict__ b, int N,
+                                                     int gpr, float *__restrict__ out) {
+    __shared__ float ts[64][65], tb[64][65];
+    const int n0 = blockIdx.x * 64, g0 = blockIdx.y * 64, t = threadIdx.x;
+    for (int i = t; i < 64 * 64; i += 256) {
+        const int r = i / 64, c = i % 64, n = n0 + r, g = g0 + c;
+        const bool ok = n < N && g < gpr;
+        const size_t src = (size_t)n * gpr + g;
+        ts[r][c] = ok ? s[src] : 0.0f;
+        tb[r][c] = ok && b ? b[src] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = t; i < 64 * 64; i += 256) {
+        const int r = i / 64, c = i % 64, g = g0 + r, n = n0 + c;
+        if (g < gpr && n < N) {
+            const float sv = ts[c][r];
+            out[((size_t)g * 2) * N + n] = sv;
+            out[((size_t)g * 2 + 1) * N + n] = __builtin_fmaf(-1024.0f, sv, tb[c][r]);
+        }
+    }
+}
 
-// Returns RQ_ERR_UNSUPPORTED (without launching) outside what k_gemm_rowwise
-// serves; the caller then uses the generic kernel.
-int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
-                const GemmWorkspace &ws, hipStream_t s) {
-    const int64_t N = w.n_out, K = w.k_in;
-    // 32-bit buffer offsets: a 256-row panel of X (256 * K * 2 bytes) must stay below 2^31.
-    if (w.format != RQ_Q_ROWWISE_I8 || xt != RQ_F16 || K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) ||
-        !aligned(x, 16) || m > 0x7fffffff || N > 0x7fffffff)
-        return RQ_ERR_UNSUPPORTED;
-    if (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)) return RQ_ERR_UNSUPPORTED;
+// f32 activations to fp16 (round to nearest even), 8 per thread per step.
+__global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, _Float16 *__restrict__ y, size_t n8) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+        const float4 a = reinterpret_cast<const float4 *>(x)[2 * i], b = reinterpret_cast<const float4 *>(x)[2 * i + 1];
+        const half8 h = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                         (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+        reinterpret_cast<half8 *>(y)[i] = h;
+    }
+}
+
+// The fp16-activation GEMM over m rows, tile chosen by shape.
+int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
+               int64_t cus, const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t N = w.n_out;
     // The largest tile whose grid still has >= 2/3 as many tiles as the device
     // has CUs: a block streams its X and W panels through one CU at a latency-
     // bound rate, so a grid that leaves CUs idle loses more than smaller tiles
@@ -702,14 +800,70 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     // 40, in 256 cache lines instead of 320 (2048x4096x4096 64.5 -> 62.1 us,
     // N = 11008 176.4 -> 171.2, K = 11008 162.5 -> 156.9 us in one run), and
     // it fills the device whenever 256x128 would.
-    const int64_t cus = num_cus > 0 ? num_cus : 256;
     // a tile taller than the tokens (rounded up to 64) only multiplies padding:
     // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
     auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (fills(128, 256)) return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, x, y, yt, m, 4, cus, ws, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, x, y, yt, m, 4, cus, ws, s);
-    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
-    return launch_tiled<64, 64, true, 4, 4, 2>(w, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 256)) return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
+    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
+    return launch_tiled<64, 64, true, 4, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
+}
+
+}  // namespace
+
+// Returns RQ_ERR_UNSUPPORTED (without launching) outside what k_gemm_rowwise
+// serves; the caller then uses the generic kernel.  Per-row int8 weights with
+// fp16 activations run directly.  Affine weights (group a multiple of 64
+// dividing k_in) and f32 activations are first prepared in the workspace's
+// preparation area (context stream only): the scales transposed to
+// [group][row] and/or the activations cast to fp16, a chunk of rows at a time
+// when they do not fit, each chunk then multiplied by the same kernel.
+int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
+                const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t N = w.n_out, K = w.k_in;
+    const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
+    // 32-bit buffer offsets: a 256-row panel of X (256 * K * 2 bytes) must stay below 2^31.
+    if (K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) || m > 0x7fffffff || N > 0x7fffffff)
+        return RQ_ERR_UNSUPPORTED;
+    if (fmt == 1 && (w.group % 64 != 0 || K % w.group != 0)) return RQ_ERR_UNSUPPORTED;
+    if (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)) return RQ_ERR_UNSUPPORTED;
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    if (fmt == 0 && xt == RQ_F16) {
+        if (!aligned(x, 16)) return RQ_ERR_UNSUPPORTED;
+        return gemm_tiles(w, w.scales, 0, x, y, yt, m, cus, ws, s);
+    }
+    if (!ws.prep || (xt == RQ_F32 && !aligned(x, 16)) || (xt == RQ_F16 && !aligned(x, 16))) return RQ_ERR_UNSUPPORTED;
+    uint8_t *prep = static_cast<uint8_t *>(ws.prep);
+    size_t used = 0;
+    const float *scales = w.scales;
+    if (fmt == 1) {
+        const int64_t gpr = K / w.group;
+        const size_t sc_bytes = ((size_t)gpr * (size_t)N * 8 + 255) & ~size_t(255);
+        if (sc_bytes > ws.prep_bytes / 2) return RQ_ERR_UNSUPPORTED;
+        float *sct = reinterpret_cast<float *>(prep);
+        hipLaunchKernelGGL(k_affine_prep, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(gpr, 64)), dim3(256), 0, s,
+                           w.scales, w.biases, (int)N, (int)gpr, sct);
+        RQ_LAUNCH_CHECK();
+        scales = sct;
+        used = sc_bytes;
+    }
+    if (xt == RQ_F16) return gemm_tiles(w, scales, fmt, x, y, yt, m, cus, ws, s);
+    // f32 activations: cast a chunk of rows (a multiple of 128) to fp16, multiply it
+    const int64_t chunk = std::min<int64_t>(m, (int64_t)((ws.prep_bytes - used) / ((size_t)K * 2)) / 128 * 128);
+    if (chunk < std::min<int64_t>(m, 128)) return RQ_ERR_UNSUPPORTED;
+    _Float16 *x16 = reinterpret_cast<_Float16 *>(prep + used);
+    const size_t eb = yt == RQ_F16 ? 2 : 4;
+    for (int64_t r0 = 0; r0 < m; r0 += chunk) {
+        const int64_t mc = std::min(chunk, m - r0);
+        const size_t n8 = (size_t)mc * (size_t)K / 8;  // K % 64 == 0
+        const unsigned blocks = (unsigned)std::min<size_t>(std::max<size_t>(cdiv((int64_t)n8, 256), 1), 8192);
+        hipLaunchKernelGGL(k_cast_f16, dim3(blocks), dim3(256), 0, s, static_cast<const float *>(x) + r0 * K, x16, n8);
+        RQ_LAUNCH_CHECK();
+        const int st = gemm_tiles(w, scales, fmt, x16, static_cast<uint8_t *>(y) + (size_t)r0 * (size_t)N * eb, yt, mc,
+                                  cus, ws, s);
+        if (st != RQ_OK) return st;
+    }
+    return RQ_OK;
 }
 
 }  // namespace rq

@@ -221,6 +221,85 @@ def test_gemm_split_k(ctx, engine, m, n, k, ydt):
     assert ok
 
 
+# ---- the reference's own inputs on the MFMA GEMM: affine weights, f32 activations ------
+# Affine u8 codes with a scale and bias per group of 64 (128) along k (the MLX format the
+# reference loads, kernels.wgsl:379-400) are expanded to fp16 u*s + b with one rounding;
+# f32 activations are cast to fp16 (round to nearest even) before the GEMM.  Both are then
+# the fp16-MFMA path, held to the fp16 bar against the f64 truth of the unrounded inputs:
+# |dy| <= 2e-3*|y| + 2e-3*max|y| (fp16 rounding of a weight or an activation is 2^-12
+# relative).  Full-size checks use sampled rows plus the all-token column checksum.
+
+def _affine(g, n, k, group=64):
+    u, s, b = synth.affine_weight(g, n, k, group)
+    return u, s, b
+
+
+def _check_rows(y, x, w_args, name):
+    rows = _sample_rows(x.shape[0])
+    truth = orc.qlinear_truth(*w_args[:3], x[rows].astype(np.float32), *w_args[3:])
+    max_abs, rel, ok = f16_tol_check(y[rows], truth)
+    report(f"{name} sampled {len(rows)} rows", max_abs, rel)
+    assert ok
+    xsum = x.astype(np.float64).sum(axis=0, keepdims=True)
+    col_truth = orc.qlinear_truth(*w_args[:3], xsum.astype(np.float32), *w_args[3:])[0]
+    col_dev = y.astype(np.float64).sum(axis=0)
+    # per-element deviations of the sampled rows, independent across tokens, bound the sum
+    dev_rms = np.sqrt(((y[rows].astype(np.float64) - truth) ** 2).mean(axis=0))
+    bound = 8 * np.sqrt(x.shape[0]) * dev_rms + 2e-3 * np.abs(col_truth) + 1e-3 * np.abs(col_truth).max()
+    assert np.all(np.abs(col_dev - col_truth) <= bound), float((np.abs(col_dev - col_truth) / bound).max())
+
+
+@pytest.mark.parametrize("xdt", [np.float16, np.float32])
+def test_config4_prefill_affine(ctx, engine, xdt):
+    g = synth.rng(4242)
+    u, s, b = _affine(g, 4096, 4096)
+    x = synth.activations(g, 2048, 4096, sigma=0.5, dtype=xdt)
+    y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float16)
+    assert np.isfinite(y).all()
+    _check_rows(y, x, (u, s, b, 1, 64), f"C4 affine g64 2048x4096x4096 x={np.dtype(xdt).name}")
+
+
+def test_config4_prefill_f32_activations(ctx, engine):
+    g = synth.rng(4243)
+    q, s = synth.rowwise_weight(g, 4096, 4096)
+    x = synth.activations(g, 2048, 4096, sigma=0.5, dtype=np.float32)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    assert np.isfinite(y).all()
+    _check_rows(y, x, (q, s, None, 0), "C4 rowwise 2048x4096x4096 x=float32")
+
+
+# every tile, split-K, group 128, and f32 activations in two chunks of the preparation area
+# (3000 x 16384 f32 -> fp16 is 98 MB: chunks of 2048 and 952 rows)
+@pytest.mark.parametrize("m,n,k,fmt,group,xdt", [
+    (17, 300, 1024, 1, 64, np.float16),     # 64x64, split-K
+    (9, 4096, 4096, 1, 64, np.float32),     # 9 tokens, f32: the GEMM (split-K)
+    (100, 1000, 1088, 1, 64, np.float32),   # 64x64, 17 k-steps
+    (300, 4096, 1024, 1, 128, np.float16),  # 128x64, group 128
+    (770, 4096, 128, 1, 64, np.float32),    # 128x128 pairs
+    (1500, 4100, 1088, 1, 64, np.float16),  # 128x256 pairs, odd k-step count
+    (1500, 4100, 1024, 0, 0, np.float32),   # rowwise, f32 activations
+    (3000, 256, 16384, 0, 0, np.float32),   # two chunks
+    (3000, 256, 16384, 1, 64, np.float32),  # two chunks, affine
+])
+def test_gemm_affine_f32_shapes(ctx, engine, m, n, k, fmt, group, xdt):
+    g = synth.rng(m * 7 + n + k + fmt)
+    if fmt == 1:
+        u, s, b = _affine(g, n, k, group)
+        w, args = QuantizedTensor.affine(ctx, u, s, b, group), (u, s, b, 1, group)
+    else:
+        q, s = synth.rowwise_weight(g, n, k)
+        w, args = QuantizedTensor.rowwise(ctx, q, s), (q, s, None, 0)
+    x = synth.activations(g, m, k, sigma=0.5, dtype=xdt)
+    y = qmm(ctx, engine, w, x, np.float32)
+    assert np.isfinite(y).all()
+    if m * k <= 2_000_000:
+        max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(*args[:3], x.astype(np.float32), *args[3:]))
+        report(f"{m}x{n}x{k} fmt={fmt} g={group} x={np.dtype(xdt).name}", max_abs, rel)
+        assert ok
+    else:
+        _check_rows(y, x, args, f"{m}x{n}x{k} fmt={fmt} g={group} x={np.dtype(xdt).name}")
+
+
 # ---- generic path, edge cases, errors -------------------------------------------
 
 @pytest.mark.parametrize("m,n,k,fmt", [(1, 50, 1000, 0), (3, 7, 33, 0), (20, 31, 100, 0), (2, 40, 96, 1),
