@@ -70,20 +70,45 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint32_t lo, uint32_t hi) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+// 8 unsigned affine codes -> fp16 u*s + b, given c = b - 1024 s: v_perm_b32
+// under exponent 0x64 gives fp16 1024 + u exactly, and fma(1024 + u, s, c) in
+// f32 is rounded once to fp16 (v_fma_mix{lo,hi}_f16).
+__device__ __forceinline__ uint32_t u8x2_affine(uint32_t u, uint32_t sel, float s, float c) {
+    const h2_t m = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, u, sel));
+    const h2_t r = {(_Float16)__builtin_fmaf((float)m.x, s, c), (_Float16)__builtin_fmaf((float)m.y, s, c)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ half8 u8x8_affine(uint32_t lo, uint32_t hi, float s, float c) {
+    uint4 r;
+    r.x = u8x2_affine(lo, 0x04010400u, s, c);
+    r.y = u8x2_affine(lo, 0x04030402u, s, c);
+    r.z = u8x2_affine(hi, 0x04010400u, s, c);
+    r.w = u8x2_affine(hi, 0x04030402u, s, c);
+    return __builtin_bit_cast(half8, r);
+}
+
 // One batch of a wave's operands: 256 k of the block's 16 weight rows, as
 // loaded (4 rows x 256 B per instruction), and the activations of the 8 MFMAs
 // that consume them (16 B per lane per MFMA, already in operand layout).
+template <int FMT>
 struct Batch {
     uint4 w[4], x[8];
+    float4 s[1], b[1];  // affine only: the four group scales / biases of MFMA row fr
 };
 
 // SWI: SwiGLU gate/up pass -- the block's 16 weight rows are 8 gate rows (W)
 // and the same 8 rows of the up weight (W2); it writes h = silu(g) * u (fp16).
-template <bool SWI, int NWV>
+// FMT 1: the reference's affine u8 codes with an f32 scale and bias per group
+// of 64 along k (K % 256 == 0): each lane loads the four group scales and
+// biases of its MFMA row for a batch (16 contiguous bytes each, beside the
+// weight loads) and expands the codes to fp16 u*s + b before the MFMA; the
+// epilogue then applies no row scale.
+template <bool SWI, int NWV, int FMT = 0>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                   const int8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                   const _Float16 *__restrict__ X, void *__restrict__ Yv, int y_f16,
-                                                  int m_act, int N, int K) {
+                                                  int m_act, int N, int K, const float *__restrict__ biases,
+                                                  const float *__restrict__ biases2) {
     constexpr int RB = SWI ? 8 : 16;  // output rows per block
     __shared__ floatx4 red[NWV][64];
     // per wave: the 16 rows x 256 k of the batch being multiplied, rows of
@@ -106,9 +131,21 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     uint8_t *wl = wt[wave];
     const int nb = (K + 255) / 256;  // 256-k batches; wave w takes batches w, w + NWV, ...
 
-    auto load = [&](Batch &b, int bi) {
+    const int Gpr = K / 64;  // affine groups per row
+    auto load = [&](Batch<FMT> &b, int bi) {
         const uint32_t k0 = (uint32_t)bi * 256u;
         const bool klive = k0 + 16u * (uint32_t)fr < (uint32_t)K;  // K % 16 == 0
+        if constexpr (FMT == 1) {
+            // MFMA row fr: weight row fr (SwiGLU: gate rows 0-7, up rows 8-15 of the same output rows)
+            const int r = SWI ? fr % 8 : fr;
+            const bool up = SWI && fr >= 8;
+            const uint32_t bytes = (uint32_t)N * (uint32_t)Gpr * 4u;
+            const uint32_t off = r < rows_here && k0 < (uint32_t)K
+                                     ? ((uint32_t)(n0 + r) * (uint32_t)Gpr + k0 / 64u) * 4u : kOOB;
+            b.s[0] = __builtin_bit_cast(float4, bload<0>(make_rsrc(up ? scales2 : scales, bytes), off));
+            const float *bp = up ? biases2 : biases;
+            b.b[0] = bp ? __builtin_bit_cast(float4, bload<0>(make_rsrc(bp, bytes), off)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the weight block
@@ -127,7 +164,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     // 8 codes of row fr at k = 32 j + 8 q, the k order of its activations.
     // Only this wave touches the slice, and LDS operations of a wave complete
     // in order, so no barrier is needed around it.
-    auto mma = [&](const Batch &b) {
+    auto mma = [&](const Batch<FMT> &b) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 4 * i + q;
@@ -139,10 +176,21 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             const int c = 2 * j + (q >> 1);
             a[j] = *reinterpret_cast<const uint2 *>(wl + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
         }
+        float sg[4], cg[4];  // affine: MFMA j covers k 32 j .. 32 j + 31, group j / 2 of the batch
+        if constexpr (FMT == 1) {
+            sg[0] = b.s[0].x; sg[1] = b.s[0].y; sg[2] = b.s[0].z; sg[3] = b.s[0].w;
+            cg[0] = __builtin_fmaf(-1024.0f, sg[0], b.b[0].x);
+            cg[1] = __builtin_fmaf(-1024.0f, sg[1], b.b[0].y);
+            cg[2] = __builtin_fmaf(-1024.0f, sg[2], b.b[0].z);
+            cg[3] = __builtin_fmaf(-1024.0f, sg[3], b.b[0].w);
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(a[j].x, a[j].y),
-                                                         __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
+        for (int j = 0; j < 8; ++j) {
+            half8 av;
+            if constexpr (FMT == 1) av = u8x8_affine(a[j].x, a[j].y, sg[j / 2], cg[j / 2]);
+            else av = i8x8_to_half8(a[j].x, a[j].y);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
+        }
     };
 
     // Two batches alternate: the next one's loads are in flight while the
@@ -152,7 +200,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     // the branch, and the prefetch is lost).  mb, the wave's batch count, is
     // wave-uniform.
     const int mb = (nb - wave + NWV - 1) / NWV;
-    Batch A, B;
+    Batch<FMT> A, B;
     if (mb > 0) {
         load(A, wave);
         int b = 0;
@@ -198,7 +246,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
                 for (int r = 0; r < 4; ++r) {
                     const int f = 4 * q + r;
                     if (f < rows_here) {
-                        const float h = silu(v[r] * scales[n0 + f]) * (u[r] * scales2[n0 + f]);
+                        const float h = FMT == 1 ? silu(v[r]) * u[r] : silu(v[r] * scales[n0 + f]) * (u[r] * scales2[n0 + f]);
                         reinterpret_cast<_Float16 *>(Yv)[(size_t)m * N + n0 + f] = (_Float16)h;
                     }
                 }
@@ -208,7 +256,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             for (int r = 0; r < 4; ++r) {
                 const int f = 4 * q + r;
                 if (f < rows_here) {
-                    const float y = v[r] * scales[n0 + f];
+                    const float y = FMT == 1 ? v[r] : v[r] * scales[n0 + f];
                     const size_t o = (size_t)m * N + n0 + f;
                     if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
                     else reinterpret_cast<float *>(Yv)[o] = y;
@@ -223,27 +271,32 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
 static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x, void *y, rq_dtype yt, int m,
                        hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
+    const bool affine = w.format == RQ_Q_AFFINE_U8;
     // 32-bit buffer offsets: 16 activation rows of K fp16 must stay below 2^31 bytes.
-    if (w.format != RQ_Q_ROWWISE_I8 || m < 1 || m > 16 || K % 16 != 0 || K > (1 << 24) || N > 0x7fffffff ||
-        !aligned(w.codes, 16) || !aligned(x, 16))
+    if (m < 1 || m > 16 || K % 16 != 0 || K > (1 << 24) || N > 0x7fffffff || !aligned(w.codes, 16) || !aligned(x, 16))
         return RQ_ERR_UNSUPPORTED;
-    if (w2 && (w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16))) return RQ_ERR_UNSUPPORTED;
+    if (affine && (w.group != 64 || K % 256 != 0 || (int64_t)N * (K / 64) * 4 > 0xffffffffll)) return RQ_ERR_UNSUPPORTED;
+    if (w2 && (w2->format != w.format || !aligned(w2->codes, 16) || (affine && w2->group != w.group)))
+        return RQ_ERR_UNSUPPORTED;
     const int64_t blocks = cdiv(N, w2 ? 8 : 16);
-    auto go = [&](auto nwv) {
-        constexpr int NW = decltype(nwv)::value;
+    auto go = [&](auto nwv, auto fmt) {
+        constexpr int NW = decltype(nwv)::value, F = decltype(fmt)::value;
         if (w2)
-            hipLaunchKernelGGL((k_gemv_mfma<true, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+            hipLaunchKernelGGL((k_gemv_mfma<true, NW, F>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
                                (const int8_t *)w.codes, w.scales, (const int8_t *)w2->codes, w2->scales,
-                               (const _Float16 *)x, y, 1, m, (int)N, (int)K);
+                               (const _Float16 *)x, y, 1, m, (int)N, (int)K, w.biases, w2->biases);
         else
-            hipLaunchKernelGGL((k_gemv_mfma<false, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+            hipLaunchKernelGGL((k_gemv_mfma<false, NW, F>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
                                (const int8_t *)w.codes, w.scales, nullptr, nullptr, (const _Float16 *)x, y,
-                               yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K);
+                               yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.biases, nullptr);
     };
-    if (K <= 4096 && blocks <= 512)
-        go(std::integral_constant<int, 8>{});
-    else
-        go(std::integral_constant<int, 4>{});
+    using I8 = std::integral_constant<int, 8>;
+    using I4 = std::integral_constant<int, 4>;
+    using F0 = std::integral_constant<int, 0>;
+    using F1 = std::integral_constant<int, 1>;
+    const bool wide = K <= 4096 && blocks <= 512;
+    if (affine) wide ? go(I8{}, F1{}) : go(I4{}, F1{});
+    else wide ? go(I8{}, F0{}) : go(I4{}, F0{});
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }

@@ -112,14 +112,29 @@ def test_gemv_tall_weights(ctx, engine, n, k):
     assert ok, (max_abs, rel)
 
 
+# m = 1-2: the dot2 GEMV; 3-16: the matrix-core GEMV in blocks of 64 rows over k slices
+# (136 rows: three row blocks, the last ragged; k = 11008 is 43 batches of 256, sliced unevenly)
 @pytest.mark.parametrize("k", [1024, 4096, 11008])
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 3, 4, 8, 12, 16])
 def test_gemv_affine_reference_format(ctx, engine, m, k):
     g = synth.rng(m + k)
     u, s, b = synth.affine_weight(g, 136, k)
     x = synth.activations(g, m, k)
     y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float16)
     max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(u, s, b, x.astype(np.float32), 1))
+    report(f"affine GEMV m={m} k={k}", max_abs, rel)
+    assert ok, (max_abs, rel)
+
+
+@pytest.mark.parametrize("m", [5, 16])
+def test_gemv_affine_4096_no_biases(ctx, engine, m):
+    # the configs[1] shape in the reference's format, and biases omitted (NULL reads as 0)
+    g = synth.rng(77 + m)
+    u, s, _ = synth.affine_weight(g, 4096, 4096)
+    x = synth.activations(g, m, 4096)
+    y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, None), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(u, s, None, x.astype(np.float32), 1))
+    report(f"affine GEMV 4096^2 m={m} no biases", max_abs, rel)
     assert ok, (max_abs, rel)
 
 

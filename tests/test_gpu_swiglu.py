@@ -108,3 +108,30 @@ def test_swiglu_shape_error(ctx, engine):
     Y = UnifiedTensor.empty(ctx, [1, 64], DType.FP16)
     with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
         engine.mlp_swiglu(ctx, X, G, U, Dbad, Y)
+
+
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_swiglu_affine_weights(ctx, engine, m):
+    """The MLP on the reference's affine weights (u8, scale + bias per 64): gate and
+    up in one matrix-core pass with the silu*mul epilogue for 3-16 tokens."""
+    g = synth.rng(500 + m)
+    inter, hidden = 320, 1024
+    ug, sg, bg = synth.affine_weight(g, inter, hidden)
+    uu, su, bu = synth.affine_weight(g, inter, hidden)
+    ud, sd, bd = synth.affine_weight(g, hidden, inter)
+    G, U, D = (QuantizedTensor.affine(ctx, *a) for a in ((ug, sg, bg), (uu, su, bu), (ud, sd, bd)))
+    x = synth.activations(g, m, hidden)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+    Y = UnifiedTensor.new(ctx, np.full((m, hidden), np.nan, np.float32), dtype=DType.FP32)
+    h = engine.mlp_swiglu(ctx, X, G, U, D, Y)
+    gt = orc.qlinear_truth(ug, sg, bg, x.astype(np.float32), 1)
+    ut = orc.qlinear_truth(uu, su, bu, x.astype(np.float32), 1)
+    with np.errstate(over="ignore"):
+        ht = (gt / (1.0 + np.exp(-gt)) * ut).astype(np.float16)
+    hd = h.to_vec().reshape(-1)[: m * inter].reshape(m, inter)
+    _, _, ok_h = f16_tol_check(hd, ht.astype(np.float64))
+    assert ok_h, "intermediate h"
+    truth = orc.qlinear_truth(ud, sd, bd, ht.astype(np.float32), 1)
+    max_abs, rel, ok = f16_tol_check(Y.to_vec(), truth)
+    print(f"[swiglu affine m={m}] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
