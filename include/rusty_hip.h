@@ -247,7 +247,9 @@ typedef struct rq_llama_config {
 } rq_llama_config;
 
 /* One LlamaBlock's weights.  Norm weights are fp16 [hidden]; Linear weights
- * are per-row int8 (RQ_Q_ROWWISE_I8) in [out, in] orientation:
+ * are per-row int8 (RQ_Q_ROWWISE_I8) or the reference's affine u8 codes
+ * (RQ_Q_AFFINE_U8, group % 16 == 0 dividing k_in; q/k/v alike in format,
+ * group and bias presence, gate/up likewise) in [out, in] orientation:
  * q [n_heads*head_dim, hidden], k/v [n_kv_heads*head_dim, hidden],
  * o [hidden, n_heads*head_dim], gate/up [intermediate, hidden],
  * down [hidden, intermediate]. */
@@ -262,7 +264,7 @@ typedef struct rq_llama_weights {
     const void *embed;             /* fp16 [vocab, hidden]                 */
     const rq_llama_layer *layers;  /* host array of n_layers               */
     const void *final_norm;        /* fp16 [hidden]                        */
-    rq_qweight lm_head;            /* int8 per-row [vocab, hidden]         */
+    rq_qweight lm_head;            /* [vocab, hidden], either format       */
 } rq_llama_weights;
 
 typedef struct rq_llama rq_llama;

@@ -8,8 +8,9 @@ It computes, in float64, the logits of every position of a token sequence
 under causal attention -- the whole sequence at once, so it shares no code
 path with the device's one-position-at-a-time KV-cache loop.  Inputs are the
 same host weights the device gets: fp16 embeddings and norm weights, per-row
-int8 codes with f32 scales (dequantized exactly, W = q * s).  No intermediate
-rounding: the reference computes in f32 throughout; the device rounds
+int8 codes with f32 scales (dequantized exactly, W = q * s) or affine u8
+codes with f32 group scales and biases (W = u * s + b, exact in f64).  No
+intermediate rounding: the reference computes in f32 throughout; the device rounds
 activations entering a GEMV and the KV cache to fp16, and its tests state the
 tolerance that allows for that.
 
@@ -33,7 +34,10 @@ invariance; rope identity at position 0, pair-norm preservation and the
 relative-position property of rotated dot products; attention against a
 single key and against equal keys; the GQA index via duplicated-KV
 equivalence with plain multi-head attention; causality (changing later
-tokens leaves earlier logits unchanged); greedy tie and threshold rules.
+tokens leaves earlier logits unchanged); greedy tie and threshold rules;
+the affine linear against the C restatement of affine_dequantize
+(oracle/oracle.py, pinned to the reference's golden vectors) and a known
+answer that fails a per-flat-index or transposed group lookup.
 """
 from __future__ import annotations
 
@@ -83,10 +87,19 @@ def silu(v: np.ndarray) -> np.ndarray:
 
 
 def linear(x: np.ndarray, qw) -> np.ndarray:
-    """x . (q * s)^T with the per-row scale applied after the exact integer-
-    weighted sum (equal to dequantizing first, in exact arithmetic)."""
-    q, s = qw
-    return (x @ q.astype(np.float64).T) * s.astype(np.float64)[None, :]
+    """Per-row int8 (q, s): x . (q * s)^T with the per-row scale applied after
+    the exact integer-weighted sum (equal to dequantizing first, in exact
+    arithmetic).  Affine u8 (u, s, b, group): x . W^T with W[n, k] =
+    u[n, k] * s[n, k // group] + b[n, k // group] (affine_dequantize,
+    kernels.wgsl:379-400; b = None means zero)."""
+    if len(qw) == 2:
+        q, s = qw
+        return (x @ q.astype(np.float64).T) * s.astype(np.float64)[None, :]
+    u, s, b, group = qw
+    n, k = u.shape
+    rep = lambda a: np.repeat(np.asarray(a, dtype=np.float64).reshape(n, k // group), group, axis=1)  # noqa: E731
+    wd = u.astype(np.float64) * rep(s) + (rep(b) if b is not None else 0.0)
+    return x @ wd.T
 
 
 def forward(cfg, w, tokens, first: int = 0) -> np.ndarray:

@@ -75,9 +75,10 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // M: activation rows (m_act <= M); CPT: chunks per thread; TPR: threads per
 // row group; R: rows per row group; FMT: 0 = ROWWISE_I8, 1 = AFFINE_U8.
-// SWI: SwiGLU gate/up pass (rowwise only) -- W/scales are the gate weight,
-// W2/scales2 the up weight of the same shape; the block loads R gate rows and
-// the same R up rows per row group and writes h = silu(g) * u (fp16).
+// SWI: SwiGLU gate/up pass -- W/scales/biases are the gate weight,
+// W2/scales2/biases2 the up weight of the same shape and format; the block
+// loads R gate rows and the same R up rows per row group and writes
+// h = silu(g) * u (fp16).
 // NORM (m = 1): the activation row is RMSNorm(x) computed in the prologue
 // from the f32 row Xf and the fp16 norm weight NW (kernels.wgsl:87-102):
 // xn = fp16((x * inv) * nw), inv = 1 / sqrt(mean(x^2) + eps).  Each block
@@ -92,11 +93,11 @@ template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA =
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
                                                     const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
+                                                    const float *__restrict__ biases2,
                                                     const _Float16 *__restrict__ X, const float *__restrict__ Xf,
                                                     const _Float16 *__restrict__ NW, float eps,
                                                     void *__restrict__ Yv, int ymode, int m_act, int N, int K,
                                                     int group, int attn_hd) {
-    static_assert(!SWI || FMT == 0, "SwiGLU pass is rowwise only");
     static_assert(!NORM || M == 1, "the fused norm serves one activation row");
     static_assert(SA == 0 || (M == 1 && !NORM && !SWI), "the attention combine serves one activation row");
     constexpr int RP = DT / TPR;
@@ -304,21 +305,30 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                       ? reinterpret_cast<const float *>(Yv)[(size_t)m * N + row0 + rin]
                       : 0.0f;
     }
-    float sg[R][CPT], bg[R][CPT];
+    // Affine: the group scale and bias of every chunk (group % 16 == 0 and
+    // K % group == 0, so a chunk sits in one group: row * (K / group) + c * 16 / group).
+    float sg[NR][CPT], bg[NR][CPT];
     if constexpr (FMT == 1) {
+        const int gk = K / group;
+        int cg[CPT];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int j = 0; j < CPT; ++j) cg[j] = (int)((unsigned)(tt + TPR * j) * 16u / (unsigned)group);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float *sp = r < R ? scales : scales2, *bp = r < R ? biases : biases2;
+            const int rin = (r % R) * RP + rp;
 #pragma unroll
             for (int j = 0; j < CPT; ++j) {
-                const int c = tt + TPR * j, rin = r * RP + rp;
+                const int c = tt + TPR * j;
                 sg[r][j] = 0.0f;
                 bg[r][j] = 0.0f;
                 if (c < C && rin < rows_here) {
-                    const size_t g = ((size_t)(row0 + rin) * K + (size_t)c * 16) / (size_t)group;
-                    sg[r][j] = scales[g];
-                    bg[r][j] = biases ? biases[g] : 0.0f;
+                    const size_t g = (size_t)(row0 + rin) * gk + cg[j];
+                    sg[r][j] = sp[g];
+                    bg[r][j] = bp ? bp[g] : 0.0f;
                 }
             }
+        }
     }
 
     // Per-chunk sums of X (fp16 dot with (1,1)); zero for chunks past K.
@@ -395,7 +405,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
         const int row = row0 + rin;
         if (lane == 0 && rin < rows_here && m < m_act) {
             float y = FMT == 0 ? tot * srow[i_t] : tot;
-            if constexpr (SWI) y = silu(y) * (tot2 * srow2[i_t]);
+            if constexpr (SWI) y = silu(y) * (FMT == 0 ? tot2 * srow2[i_t] : tot2);
             const size_t o = (size_t)m * N + row;
             if (ymode == kYF16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
             else if (ymode == kYAdd) reinterpret_cast<float *>(Yv)[o] = yold[i_t] + y;
@@ -405,7 +415,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 }
 
 using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
-                          const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int,
+                          const float *, const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int,
                           int);
 
 // A kernel instance and the rows per row group (R) it was compiled for; the
@@ -433,48 +443,54 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //  m = 2..4: 4 (SwiGLU: 2 pairs).
 //   * attention-combine prologue: 4 (each block re-reads the partials, so
 //     fewer, larger blocks).
-// fmt 2 selects the SwiGLU gate/up pass; norm (m = 1, per-row codes only)
-// the fused RMSNorm prologue; sa (m = 1, per-row codes) the attention combine
-// of sa partials per head.
-template <int M, int CPT, int TPR>
-Decode pick_fmt(int fmt, bool norm, bool tall, int sa) {
+// fmt: 0 = per-row int8, 1 = affine u8; swi selects the SwiGLU gate/up
+// pass; norm (m = 1) the fused RMSNorm prologue; sa (m = 1) the attention
+// combine of sa partials per head.
+template <int M, int CPT, int TPR, int FMT>
+Decode pick_fmt(bool swi, bool norm, bool tall, int sa) {
     if constexpr (M == 1) {
         constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
         constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
-        constexpr int RP = CPT >= 2 ? 4 : 2;     // plain per-row codes
-        if (sa == 1) return inst<1, CPT, TPR, 4, 0, false, false, 1>();
-        if (sa == 2) return inst<1, CPT, TPR, 4, 0, false, false, 2>();
-        if (sa == 4) return inst<1, CPT, TPR, 4, 0, false, false, 4>();
-        if (sa == 8) return inst<1, CPT, TPR, 4, 0, false, false, 8>();
-        if (fmt == 2) return norm ? inst<1, CPT, TPR, RSN, 0, true, true>() : inst<1, CPT, TPR, 2, 0, true, false>();
-        if (fmt == 0 && tall) return norm ? inst<1, CPT, TPR, 8, 0, false, true>() : inst<1, CPT, TPR, 8, 0, false, false>();
-        if (norm) return inst<1, CPT, TPR, RN, 0, false, true>();
-        return fmt == 0 ? inst<1, CPT, TPR, RP, 0, false, false>() : inst<1, CPT, TPR, 2, 1, false, false>();
+        constexpr int RP = FMT == 0 && CPT >= 2 ? 4 : 2;
+        if (sa == 1) return inst<1, CPT, TPR, 4, FMT, false, false, 1>();
+        if (sa == 2) return inst<1, CPT, TPR, 4, FMT, false, false, 2>();
+        if (sa == 4) return inst<1, CPT, TPR, 4, FMT, false, false, 4>();
+        if (sa == 8) return inst<1, CPT, TPR, 4, FMT, false, false, 8>();
+        if (swi) return norm ? inst<1, CPT, TPR, RSN, FMT, true, true>() : inst<1, CPT, TPR, 2, FMT, true, false>();
+        if (FMT == 0 && tall)
+            return norm ? inst<1, CPT, TPR, 8, FMT, false, true>() : inst<1, CPT, TPR, 8, FMT, false, false>();
+        if (norm) return inst<1, CPT, TPR, RN, FMT, false, true>();
+        return inst<1, CPT, TPR, RP, FMT, false, false>();
     } else {
         (void)norm;
         (void)tall;
         (void)sa;
-        if (fmt == 2) return inst<M, CPT, TPR, 2, 0, true, false>();
-        return fmt == 0 ? inst<M, CPT, TPR, 4, 0, false, false>() : inst<M, CPT, TPR, 4, 1, false, false>();
+        if (swi) return inst<M, CPT, TPR, 2, FMT, true, false>();
+        return inst<M, CPT, TPR, 4, FMT, false, false>();
     }
 }
 
+template <int M, int CPT, int TPR>
+Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa) {
+    return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa) : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa);
+}
+
 template <int M, int CPT>
-Decode pick_tpr(int tpr, int fmt, bool norm, bool tall, int sa) {
+Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa) {
     switch (tpr) {
-    case 64: return pick_fmt<M, CPT, 64>(fmt, norm, tall, sa);
-    case 128: return pick_fmt<M, CPT, 128>(fmt, norm, tall, sa);
-    default: return pick_fmt<M, CPT, 256>(fmt, norm, tall, sa);
+    case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa);
+    case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa);
+    default: return pick_swi<M, CPT, 256>(fmt, swi, norm, tall, sa);
     }
 }
 
 template <int M>
-Decode pick_cpt(int cpt, int tpr, int fmt, bool norm, bool tall, int sa) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa) {
     switch (cpt) {
-    case 1: return pick_tpr<M, 1>(tpr, fmt, norm, tall, sa);
-    case 2: return pick_tpr<M, 2>(tpr, fmt, norm, tall, sa);
-    case 3: return pick_tpr<M, 3>(tpr, fmt, norm, tall, sa);
-    default: return pick_tpr<M, 4>(tpr, fmt, norm, tall, sa);
+    case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa);
+    case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa);
+    case 3: return pick_tpr<M, 3>(tpr, fmt, swi, norm, tall, sa);
+    default: return pick_tpr<M, 4>(tpr, fmt, swi, norm, tall, sa);
     }
 }
 
@@ -487,29 +503,29 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
                          void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0) {
     const int64_t N = w.n_out, K = w.k_in;
     if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
-        !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && w.group % 16 != 0))
+        !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && (w.group % 16 != 0 || K % w.group != 0)))
         return RQ_ERR_UNSUPPORTED;
-    if (w2 && (w.format != RQ_Q_ROWWISE_I8 || w2->format != RQ_Q_ROWWISE_I8 || !aligned(w2->codes, 16)))
+    if (w2 && (w2->format != w.format || w2->group != w.group || !aligned(w2->codes, 16)))
         return RQ_ERR_UNSUPPORTED;
-    if (nw && (m != 1 || w.format != RQ_Q_ROWWISE_I8 || !aligned(nw, 16))) return RQ_ERR_UNSUPPORTED;
-    if (sa && (m != 1 || w2 || nw || w.format != RQ_Q_ROWWISE_I8 || (sa != 1 && sa != 2 && sa != 4 && sa != 8) ||
-               attn_hd < 8 || attn_hd % 8 != 0 || K % attn_hd != 0))
+    if (nw && (m != 1 || !aligned(nw, 16))) return RQ_ERR_UNSUPPORTED;
+    if (sa && (m != 1 || w2 || nw || (sa != 1 && sa != 2 && sa != 4 && sa != 8) || attn_hd < 8 ||
+               attn_hd % 8 != 0 || K % attn_hd != 0))
         return RQ_ERR_UNSUPPORTED;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
     const int cpt = (int)cdiv(C, tpr);
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
-    const int fmt = w2 ? 2 : w.format;
-    const bool norm = nw != nullptr;
-    const bool tall = mt == 1 && !w2 && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, norm, tall, sa)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, false, false, 0)
-                                       : pick_cpt<4>(cpt, tpr, fmt, false, false, 0);
+    const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
+    const bool swi = w2 != nullptr, norm = nw != nullptr;
+    const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0)
+                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0);
     const bool fx = norm || sa;  // x is an f32 source read by the prologue
     const int rows = d.r * (DT / tpr);
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
-                       w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr,
+                       w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, w2 ? w2->biases : nullptr,
                        fx ? nullptr : (const _Float16 *)x, fx ? (const float *)x : nullptr, nw, eps, y, ymode, m,
                        (int)N, (int)K, w.group, attn_hd);
     RQ_LAUNCH_CHECK();

@@ -1,4 +1,4 @@
-// Int8-weight Llama decode runner: one greedy decode step of a LlamaModel
+// Quantized-weight Llama decode runner (per-row int8 or affine u8 Linears): one greedy decode step of a LlamaModel
 // (rusty-graph/src/lib.rs:420-436) as a HIP graph of 5 launches per block
 // plus 2 at the end, replayed once per token with no host round trip.
 //
@@ -446,19 +446,29 @@ int enqueue_step(rq_llama *md, hipStream_t s) {
     return RQ_OK;
 }
 
-// The decode kernels this runner launches take per-row int8 weights with
-// K % 16 == 0 and K <= 16384, 16-byte aligned codes.
+// The decode kernels this runner launches take per-row int8 or affine u8
+// weights (affine: group % 16 == 0 and k % group == 0) with k % 16 == 0,
+// k <= 16384 and 16-byte aligned codes.
 int check_linear(const rq_qweight &w, int64_t n, int64_t k, const char *name, int layer) {
     int st = check_qweight(&w);
     if (st != RQ_OK) return st;
     if (w.n_out != n || w.k_in != k)
         return fail(RQ_ERR_SHAPE, "layer %d %s: weight is [%lld,%lld], expected [%lld,%lld]", layer, name,
                     (long long)w.n_out, (long long)w.k_in, (long long)n, (long long)k);
-    if (w.format != RQ_Q_ROWWISE_I8)
-        return fail(RQ_ERR_UNSUPPORTED, "layer %d %s: the decode runner takes per-row int8 weights", layer, name);
+    if (w.format == RQ_Q_AFFINE_U8 && (w.group % 16 != 0 || k % w.group != 0))
+        return fail(RQ_ERR_UNSUPPORTED, "layer %d %s: affine weights need group %% 16 == 0 and k %% group == 0",
+                    layer, name);
     if (k % 16 != 0 || k > 16384 || !aligned(w.codes, 16))
         return fail(RQ_ERR_UNSUPPORTED, "layer %d %s: needs k %% 16 == 0, k <= 16384 and 16-byte aligned codes",
                     layer, name);
+    return RQ_OK;
+}
+
+// Weights fused into one launch (q/k/v, gate/up) share format, group and the
+// presence of biases.
+int check_same(const rq_qweight &a, const rq_qweight &b, const char *what, int layer) {
+    if (a.format != b.format || (a.format == RQ_Q_AFFINE_U8 && (a.group != b.group || !a.biases != !b.biases)))
+        return fail(RQ_ERR_UNSUPPORTED, "layer %d: %s weights differ in format, group or biases", layer, what);
     return RQ_OK;
 }
 
@@ -519,7 +529,8 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
         if ((st = check_linear(L.q, QW, H, "q_proj", l)) || (st = check_linear(L.k, KW, H, "k_proj", l)) ||
             (st = check_linear(L.v, KW, H, "v_proj", l)) || (st = check_linear(L.o, H, QW, "o_proj", l)) ||
             (st = check_linear(L.gate, I, H, "gate_proj", l)) || (st = check_linear(L.up, I, H, "up_proj", l)) ||
-            (st = check_linear(L.down, H, I, "down_proj", l)))
+            (st = check_linear(L.down, H, I, "down_proj", l)) || (st = check_same(L.q, L.k, "q/k/v", l)) ||
+            (st = check_same(L.q, L.v, "q/k/v", l)) || (st = check_same(L.gate, L.up, "gate/up", l)))
             return st;
     }
     if ((st = check_linear(w->lm_head, c.vocab, H, "lm_head", -1))) return st;
@@ -532,10 +543,17 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     md->final_norm = static_cast<const _Float16 *>(w->final_norm);
     md->lm_head = w->lm_head;
 
-    // one allocation: per layer packed [q;k;v] codes and scales, then state
+    // one allocation: per layer packed [q;k;v] codes, scales (and biases),
+    // then state; affine scales hold H / group entries per row
     const size_t L = (size_t)c.n_layers, kv = L * (size_t)c.n_kv_heads * c.max_seq * c.head_dim;
     auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
-    size_t bytes = L * (pad((size_t)QKV * H) + pad((size_t)QKV * 4));
+    std::vector<size_t> per_row(L);  // scale entries per row of each layer's q/k/v
+    size_t bytes = 0;
+    for (size_t l = 0; l < L; ++l) {
+        const rq_qweight &q = w->layers[l].q;
+        per_row[l] = q.format == RQ_Q_AFFINE_U8 ? (size_t)(H / q.group) : 1;
+        bytes += pad((size_t)QKV * H) + pad((size_t)QKV * per_row[l] * 4) * (q.biases ? 2 : 1);
+    }
     // attention splits: ~160 positions of the cache per block up to 480 (each
     // block's K/V rows stream through one CU), 8 beyond (for 640 positions 8
     // splits measured 1.7 % more tokens/s than 4, with the o-projection
@@ -557,21 +575,26 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     for (size_t l = 0; l < L; ++l) {
         const rq_llama_layer &src = w->layers[l];
         rq_llama::Layer &dst = md->layers[l];
+        const size_t pr = per_row[l];
         uint8_t *codes = carve<uint8_t>(p, (size_t)QKV * H);
-        float *scales = carve<float>(p, (size_t)QKV);
+        float *scales = carve<float>(p, (size_t)QKV * pr);
+        float *biases = src.q.biases ? carve<float>(p, (size_t)QKV * pr) : nullptr;
         const rq_qweight *parts[3] = {&src.q, &src.k, &src.v};
         size_t row = 0;
         for (const rq_qweight *pw : parts) {
-            e = hipMemcpyAsync(codes + row * H, pw->codes, (size_t)pw->n_out * H, hipMemcpyDeviceToDevice, s);
+            const size_t n = (size_t)pw->n_out;
+            e = hipMemcpyAsync(codes + row * H, pw->codes, n * H, hipMemcpyDeviceToDevice, s);
             if (e == hipSuccess)
-                e = hipMemcpyAsync(scales + row, pw->scales, (size_t)pw->n_out * 4, hipMemcpyDeviceToDevice, s);
+                e = hipMemcpyAsync(scales + row * pr, pw->scales, n * pr * 4, hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess && biases)
+                e = hipMemcpyAsync(biases + row * pr, pw->biases, n * pr * 4, hipMemcpyDeviceToDevice, s);
             if (e != hipSuccess) {
                 release(md);
                 return fail(RQ_ERR_HIP, "packing q/k/v: %s", hipGetErrorString(e));
             }
-            row += (size_t)pw->n_out;
+            row += n;
         }
-        dst.qkv = rq_qweight{codes, scales, nullptr, QKV, H, RQ_Q_ROWWISE_I8, 0};
+        dst.qkv = rq_qweight{codes, scales, biases, QKV, H, src.q.format, src.q.group};
         dst.o = src.o;
         dst.gate = src.gate;
         dst.up = src.up;

@@ -1,12 +1,14 @@
-"""Greedy int8-weight Llama decode on the device (``rq_llama_*`` of the C ABI).
+"""Greedy quantized-weight Llama decode on the device (``rq_llama_*`` of the C ABI).
 
 Host mirror of the reference's ``LlamaModel`` (rusty-graph/src/lib.rs:410-436):
 token embedding (fp16 table), ``n_layers`` LlamaBlocks (RMSNorm -> GQA
 attention with RoPE and a KV cache -> residual add -> RMSNorm -> SwiGLU MLP ->
 residual add, lib.rs:364-378), final RMSNorm and the lm_head projection, with
-greedy (top-1) sampling.  Every Linear is a per-row int8 weight read by the
-fused dequant-GEMV; the whole step runs as one HIP graph on the device
-(librusty_hip.so), with no host round trip between tokens.
+greedy (top-1) sampling.  Every Linear is a quantized weight read by the
+fused dequant-GEMV (per-row int8, or the reference's affine u8 codes as an
+MLX checkpoint holds them: ``load_mlx``); the whole step runs as one HIP
+graph on the device (librusty_hip.so), with no host round trip between
+tokens.
 
 The reference has no decode loop (its LlamaModel::forward takes the ids and a
 KV cache but nothing drives generation); the loop defined here is: prefill the
@@ -62,8 +64,10 @@ LLAMA_1B = LlamaConfig()
 
 @dataclass
 class LlamaHostWeights:
-    """Host copies: fp16 embed [V,H] and norms [H]; per-row int8 Linears as
-    (codes int8 [out,in], scales f32 [out])."""
+    """Host copies: fp16 embed [V,H] and norms [H]; each Linear either per-row
+    int8 as (codes int8 [out,in], scales f32 [out]) or the reference's affine
+    u8 as (codes uint8 [out,in], scales f32 [out, in/group], biases f32
+    [out, in/group] or None, group)."""
     embed: np.ndarray
     layers: list[dict] = field(default_factory=list)
     final_norm: np.ndarray | None = None
@@ -99,6 +103,110 @@ def synth_weights(cfg: LlamaConfig, seed: int = 0) -> LlamaHostWeights:
     return w
 
 
+# Weight names tried in order: the reference's (rusty-graph/src/model_builder.rs:
+# 145-206: feed_forward.w1/w3/w2, self_attn.out_proj, operator_norm/ffn_norm),
+# then the usual MLX Llama names.
+_NAMES = {
+    "q": ("self_attn.q_proj",), "k": ("self_attn.k_proj",), "v": ("self_attn.v_proj",),
+    "o": ("self_attn.out_proj", "self_attn.o_proj"),
+    "gate": ("feed_forward.w1", "mlp.gate_proj"), "up": ("feed_forward.w3", "mlp.up_proj"),
+    "down": ("feed_forward.w2", "mlp.down_proj"),
+    "attn_norm": ("operator_norm", "input_layernorm"), "mlp_norm": ("ffn_norm", "post_attention_layernorm"),
+}
+
+
+def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaHostWeights]:
+    """A Llama checkpoint in MLX's 8-bit affine layout (``config.json`` +
+    ``*.safetensors``) as runner inputs.
+
+    Follows ModelBuilder (rusty-graph/src/model_builder.rs): a weight with a
+    ``.scales`` tensor is quantized (load_tensor, :68-82) and its codes,
+    scales and biases are kept as they are (the reference dequantizes them to
+    f32; here the fused kernels read them); norms are plain tensors
+    (build_rms_norm, :140-143); the final norm is ``model.norm`` or else
+    ``model.embedding_norm`` (:234-240); without ``lm_head.weight`` the
+    embedding is tied to the lm_head (:242-249).  The runner's embedding table
+    is fp16: a quantized ``model.embed_tokens`` is dequantized on the host
+    (u * s + b in f64) and rounded to fp16, norms are rounded to fp16.
+    ``max_seq`` defaults to ``max_position_embeddings`` (else 2048)."""
+    from pathlib import Path
+
+    from .loader import LoaderError, QuantizationConfig, WeightsContext, load_config
+
+    model_dir = Path(model_dir)
+    conf = load_config(model_dir / "config.json")
+    quant = conf.get("quantization") or QuantizationConfig()
+    heads = int(conf["num_attention_heads"])
+    hidden = int(conf["hidden_size"])
+    cfg = LlamaConfig(
+        n_layers=int(conf["num_hidden_layers"]), hidden=hidden, n_heads=heads,
+        n_kv_heads=int(conf.get("num_key_value_heads") or heads),
+        head_dim=int(conf.get("head_dim") or hidden // heads), intermediate=int(conf["intermediate_size"]),
+        vocab=int(conf["vocab_size"]),
+        max_seq=int(max_seq or conf.get("max_position_embeddings") or 2048),
+        norm_eps=float(conf.get("norm_eps", conf.get("rms_norm_eps", 1e-5))),
+        rope_theta=float(conf.get("rope_theta", 10000.0)))
+    wc = WeightsContext()
+    files = sorted(model_dir.glob("*.safetensors"))
+    if not files:
+        raise LoaderError(f"{model_dir}: no .safetensors files")
+    for f in files:
+        wc.load_file(f)
+
+    def quantized(name):
+        if wc.get_tensor_info(f"{name}.scales") is None:
+            raise LoaderError(f"{name}: the runner takes quantized Linears (no {name}.scales)")
+        codes, sc, b = wc._quantized_host(name, quant)
+        n, k = codes.shape
+        return codes, sc.reshape(n, k // quant.group_size), b.reshape(n, k // quant.group_size), quant.group_size
+
+    def plain(name):
+        a, _ = wc.read_bytes(f"{name}.weight")
+        dt = wc.get_tensor_info(f"{name}.weight")[1]
+        if dt == "BF16":
+            return (a.astype(np.uint32) << 16).view(np.float32)
+        if dt not in ("F32", "F16"):
+            raise LoaderError(f"{name}.weight: expected F32, F16 or BF16, got {dt}")
+        return a.astype(np.float32)
+
+    def pick(prefix, key):
+        for n in _NAMES[key]:
+            name = f"{prefix}.{n}"
+            if wc.get_tensor_info(f"{name}.weight") is not None:
+                return name
+        raise LoaderError(f"{prefix}: none of {', '.join(_NAMES[key])} found")
+
+    try:
+        if wc.get_tensor_info("model.embed_tokens.scales") is not None:
+            codes, sc, b, gs = quantized("model.embed_tokens")
+            tied = (codes, sc, b, gs)
+            rep = lambda a: np.repeat(a.astype(np.float64), gs, axis=1)  # noqa: E731
+            embed = (codes * rep(sc) + rep(b)).astype(np.float16)
+        else:
+            tied = None
+            embed = plain("model.embed_tokens").astype(np.float16)
+        w = LlamaHostWeights(embed=embed.reshape(cfg.vocab, cfg.hidden))
+        for i in range(cfg.n_layers):
+            pre = f"model.layers.{i}"
+            layer = {}
+            for key in ("attn_norm", "mlp_norm"):
+                layer[key] = plain(pick(pre, key)).astype(np.float16)
+            for key in ("q", "k", "v", "o", "gate", "up", "down"):
+                layer[key] = quantized(pick(pre, key))
+            w.layers.append(layer)
+        final = "model.norm" if wc.get_tensor_info("model.norm.weight") is not None else "model.embedding_norm"
+        w.final_norm = plain(final).astype(np.float16)
+        if wc.get_tensor_info("lm_head.weight") is not None:
+            w.lm_head = quantized("lm_head")
+        elif tied is not None:
+            w.lm_head = tied
+        else:
+            raise LoaderError("tied lm_head needs a quantized model.embed_tokens")
+    finally:
+        wc.close()
+    return cfg, w
+
+
 class LlamaRunner:
     """Device-resident model + KV cache + captured step graph."""
 
@@ -111,8 +219,9 @@ class LlamaRunner:
             self._keep.append(t)
             return t.ptr
 
-        def dev_q(pair):
-            qt = QuantizedTensor.rowwise(ctx, *pair)
+        def dev_q(lin):
+            qt = QuantizedTensor.rowwise(ctx, *lin) if len(lin) == 2 else QuantizedTensor.affine(
+                ctx, lin[0], lin[1], lin[2], group=lin[3])
             self._keep.append(qt)
             return qt.descriptor()
 

@@ -1,4 +1,4 @@
-"""GPU parity of the int8 Llama decode runner (rq_llama_*) against the oracle.
+"""GPU parity of the quantized-weight Llama decode runner (rq_llama_*) against the oracle.
 
 The device runs the sequence one position at a time through its KV cache
 (one graph launch per token); the oracle (oracle/llama.py) runs the whole
@@ -17,7 +17,8 @@ import pytest
 
 from oracle import llama as ol
 from rusty_amd import RqError
-from rusty_amd.llama import LLAMA_1B, LlamaConfig, LlamaRunner, synth_weights
+from mlx_files import write_mlx_llama
+from rusty_amd.llama import LLAMA_1B, LlamaConfig, LlamaRunner, load_mlx, synth_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +79,39 @@ def test_small_models_match_oracle(ctx, cfg):
     with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
         r.decode(1)
     r.close()
+
+
+@pytest.mark.parametrize("cfg,names,tie", [
+    (TINY, "reference", True),
+    (LlamaConfig(n_layers=2, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, intermediate=384, vocab=777,
+                 max_seq=200), "mlx", False),
+], ids=["reference_names_tied", "mlx_names_hd128"])
+def test_mlx_checkpoint_decodes(ctx, tmp_path, cfg, names, tie):
+    """An MLX 8-bit affine checkpoint (u8 codes, bf16 scale + bias per 64)
+    loaded by load_mlx decodes through the runner on the affine codes
+    themselves (fused norm, attention-combine and SwiGLU prologues of the
+    decode GEMV), against the oracle on the same weights."""
+    write_mlx_llama(tmp_path, cfg, seed=cfg.hidden, names=names, tie=tie)
+    lcfg, w = load_mlx(tmp_path)
+    assert lcfg == cfg and len(w.layers[0]["q"]) == 4
+    g = np.random.default_rng(31)
+    n_prompt = 40
+    prompt = g.integers(0, cfg.vocab, n_prompt)
+    r = LlamaRunner(ctx, lcfg, w)
+    toks, logits = run_collect(r, prompt, cfg.max_seq - n_prompt)
+    np.testing.assert_array_equal(toks[:n_prompt], prompt)
+    check_steps(cfg, w, toks, logits, n_prompt, 1e-2, f"mlx {names}")
+    r.close()
+
+
+def test_mixed_qkv_formats_refused(ctx):
+    w = synth_weights(TINY, seed=25)
+    g = np.random.default_rng(26)
+    n, k = TINY.linear_shapes()["k"]
+    w.layers[0]["k"] = (g.integers(0, 256, (n, k), dtype=np.uint8), np.full((n, k // 64), 1e-4, np.float32),
+                        np.full((n, k // 64), -128e-4, np.float32), 64)
+    with pytest.raises(RqError, match="RQ_ERR_UNSUPPORTED"):
+        LlamaRunner(ctx, TINY, w)
 
 
 def test_restart_and_single_token_prompt(ctx):

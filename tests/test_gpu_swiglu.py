@@ -110,12 +110,14 @@ def test_swiglu_shape_error(ctx, engine):
         engine.mlp_swiglu(ctx, X, G, U, Dbad, Y)
 
 
-@pytest.mark.parametrize("m", [1, 8, 16])
-def test_swiglu_affine_weights(ctx, engine, m):
+@pytest.mark.parametrize("m,hidden", [(1, 1024), (2, 1024), (1, 4096), (2, 2560), (8, 1024), (16, 1024)])
+def test_swiglu_affine_weights(ctx, engine, m, hidden):
     """The MLP on the reference's affine weights (u8, scale + bias per 64): gate and
-    up in one matrix-core pass with the silu*mul epilogue for 3-16 tokens."""
-    g = synth.rng(500 + m)
-    inter, hidden = 320, 1024
+    up in one pass with the silu*mul epilogue -- the decode kernel's SwiGLU pass
+    for 1-2 tokens (row groups of 64/256 threads, 1-3 chunks per thread), the
+    matrix-core pass for 3-16."""
+    g = synth.rng(500 + m + hidden)
+    inter = 320
     ug, sg, bg = synth.affine_weight(g, inter, hidden)
     uu, su, bu = synth.affine_weight(g, inter, hidden)
     ud, sd, bd = synth.affine_weight(g, hidden, inter)
