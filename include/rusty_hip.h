@@ -274,9 +274,19 @@ typedef struct rq_llama rq_llama;
 int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weights *w, rq_llama **out);
 int rq_llama_destroy(rq_llama *model);
 /* Starts a sequence: runs the n prompt tokens (host array, each < vocab)
- * through the model one position at a time, filling the KV cache; the last
- * step's greedy token becomes token n of the sequence.  Asynchronous. */
+ * through the model, filling the KV cache; the greedy token of the last
+ * position becomes token n of the sequence.  By default the prompt runs in
+ * batched chunks (every position of a chunk at once: [rows, hidden] GEMMs
+ * and a causal prefill attention); see rq_llama_set_prefill.  Uses the
+ * context's GEMM workspace when `stream` is the context stream (NULL), so
+ * runs on other streams must not overlap other GEMM work of the context.
+ * Asynchronous apart from the token upload. */
 int rq_llama_prefill(rq_llama *model, const int32_t *tokens, int32_t n, rq_stream stream);
+/* Positions per batched prefill chunk: a multiple of 32 up to
+ * min(max_seq rounded up to 32, 2048) (the default), or 0 to run the prompt
+ * one position at a time through the decode step (the step graph).
+ * No reference counterpart (the reference has no prompt loop). */
+int rq_llama_set_prefill(rq_llama *model, int32_t rows);
 /* n_steps greedy decode steps, each feeding the previous token.  The
  * sequence grows by n_steps; fails with RQ_ERR_SHAPE past max_seq cached
  * positions.  Asynchronous (graph launches only). */

@@ -116,6 +116,7 @@ _SIGNATURES = {
     "rq_llama_prefill": [_P, POINTER(c_int32), c_int32, _P],
     "rq_llama_decode": [_P, c_int32, _P],
     "rq_llama_set_graph": [_P, c_int],
+    "rq_llama_set_prefill": [_P, c_int32],
     "rq_llama_tokens": [_P, POINTER(c_int32), c_int32, POINTER(c_int32), _P],
     "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }

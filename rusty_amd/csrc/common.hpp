@@ -119,6 +119,21 @@ int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_
 int launch_qmatmul_dx(const rq_qweight &w, const void *dy, rq_dtype dyt, void *dx, rq_dtype dxt, int64_t m,
                       hipStream_t s);
 
+// Batched prompt kernels of the Llama runner (one launch each over n rows).
+// x[s] = f32(embed[tokens[s]]) for s < n.
+int launch_embed_rows(const int *tokens, const _Float16 *embed, int H, float *x, int n, hipStream_t s);
+// x[s] += y[s] (y may be null), then xn[s] = fp16(rmsnorm(x[s]) * nw) (nw null: add only).
+int launch_add_rmsnorm_rows(float *x, const float *y, const _Float16 *nw, float eps, _Float16 *xn, int n, int H,
+                            hipStream_t s);
+// RoPE of rows p0..p0+n-1 of qkv (f32 [n][(n_heads + 2 n_kv) hd]): q to fp16
+// [n][n_heads][hd], k and v (fp16) into one layer's cache [n_kv][max_seq][hd].
+int launch_rope_scatter(const float *qkv, const float2 *rope, int p0, int n, int n_heads, int n_kv, int hd,
+                        int max_seq, _Float16 *q, _Float16 *kc, _Float16 *vc, hipStream_t s);
+// Causal attention of the n queries at positions p0.. (p0 % 32 == 0) over
+// cache positions 0..p0+n-1; out fp16 [n][n_heads * hd].
+int launch_attn_prefill(const _Float16 *q, const _Float16 *kc, const _Float16 *vc, _Float16 *out, int p0, int n,
+                        int n_heads, int n_kv, int hd, int max_seq, hipStream_t s);
+
 // Y = X . deq(W)^T over every kernel family, picked by m, dtypes and shape.
 int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
                      hipStream_t s);

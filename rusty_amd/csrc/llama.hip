@@ -27,6 +27,7 @@
 // fp16; the KV cache is fp16 in [layer][kv_head][position][head_dim] order.
 #include <math.h>
 
+#include <algorithm>
 #include <new>
 #include <type_traits>
 #include <vector>
@@ -50,6 +51,14 @@ struct rq_llama {
     _Float16 *h = nullptr, *kc = nullptr, *vc = nullptr;
     int *tokens = nullptr, *pos = nullptr, *n_prompt = nullptr;
     float2 *rope = nullptr;  // (cos, sin) per position and rotated pair
+    // batched prompt buffers, prefill_cap rows: residual rows x and projection
+    // outputs y (f32 [rows][H]), normalised rows xn (fp16 [rows][H]), q/k/v
+    // (f32 [rows][QKV]), roped q and the attention output (fp16
+    // [rows][n_heads * head_dim]), SwiGLU workspace h (fp16 [2][rows][I])
+    float *px = nullptr, *py = nullptr, *pqkv = nullptr;
+    _Float16 *pxn = nullptr, *pq = nullptr, *patt = nullptr, *ph = nullptr;
+    int prefill_cap = 0;   // rows the buffers hold
+    int prefill_rows = 0;  // rows per batched chunk; 0: one position at a time through the step graph
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
@@ -62,6 +71,9 @@ namespace {
 
 constexpr int NT = 256;
 constexpr int kMaxSeq = 32768;  // KV cache capacity limit (32-bit cache offsets)
+// Rows of a batched prompt chunk: prompts up to this many positions (and
+// max_seq) run as one chunk of [rows, H] GEMMs, longer ones in chunks.
+constexpr int kPrefillRows = 2048;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -413,6 +425,13 @@ __global__ __launch_bounds__(NT) void k_embed_start(const int *__restrict__ toke
     }
 }
 
+// The step state after a batched prompt: the last prompt position was
+// processed (pos) and the prompt has n tokens.
+__global__ void k_set_position(int *__restrict__ pos_p, int *__restrict__ n_prompt_p, int pos, int n) {
+    *pos_p = pos;
+    *n_prompt_p = n;
+}
+
 int enqueue_step(rq_llama *md, hipStream_t s) {
     const rq_llama_config &c = md->cfg;
     const int H = c.hidden;
@@ -469,6 +488,50 @@ int check_linear(const rq_qweight &w, int64_t n, int64_t k, const char *name, in
 int check_same(const rq_qweight &a, const rq_qweight &b, const char *what, int layer) {
     if (a.format != b.format || (a.format == RQ_Q_AFFINE_U8 && (a.group != b.group || !a.biases != !b.biases)))
         return fail(RQ_ERR_UNSUPPORTED, "layer %d: %s weights differ in format, group or biases", layer, what);
+    return RQ_OK;
+}
+
+// Prompt positions p0..p0+n-1 (tokens already in md->tokens) through every
+// layer at once: [n, H] GEMMs, the causal prefill attention writing the KV
+// cache.  The last chunk (end) also computes the logits of position p0+n-1
+// and appends the greedy token, leaving the step state where the decode
+// steps continue (x = its embedding, pos = p0 + n).
+int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
+    const rq_llama_config &c = md->cfg;
+    const int H = c.hidden;
+    const size_t kv_layer = (size_t)c.n_kv_heads * c.max_seq * c.head_dim;
+    const GemmWorkspace ws = gemm_workspace(md->ctx, s);
+    int st;
+    if ((st = launch_embed_rows(md->tokens + p0, md->embed, H, md->px, n, s)) != RQ_OK) return st;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const rq_llama::Layer &L = md->layers[l];
+        // x += (previous layer's down projection), xn = rmsnorm(x)
+        if ((st = launch_add_rmsnorm_rows(md->px, l ? md->py : nullptr, L.attn_norm, c.norm_eps, md->pxn, n, H, s)))
+            return st;
+        if ((st = qmatmul_dispatch(md->ctx, L.qkv, md->pxn, RQ_F16, md->pqkv, RQ_F32, n, s))) return st;
+        _Float16 *kc = md->kc + l * kv_layer, *vc = md->vc + l * kv_layer;
+        if ((st = launch_rope_scatter(md->pqkv, md->rope, p0, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
+                                      md->pq, kc, vc, s)))
+            return st;
+        if ((st = launch_attn_prefill(md->pq, kc, vc, md->patt, p0, n, c.n_heads, c.n_kv_heads, c.head_dim,
+                                      c.max_seq, s)))
+            return st;
+        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt, RQ_F16, md->py, RQ_F32, n, s))) return st;
+        if ((st = launch_add_rmsnorm_rows(md->px, md->py, L.mlp_norm, c.norm_eps, md->pxn, n, H, s))) return st;
+        if ((st = swiglu_run(md->ctx, L.gate, L.up, L.down, md->pxn, RQ_F16, md->ph, md->py, RQ_F32, n, ws, s)))
+            return st;
+    }
+    if (!end) return RQ_OK;
+    // the last position only: x += down projection, logits, greedy pick
+    float *xl = md->px + (size_t)(n - 1) * H;
+    if ((st = launch_add_rmsnorm_rows(xl, md->py + (size_t)(n - 1) * H, nullptr, 0.0f, nullptr, 1, H, s))) return st;
+    if ((st = launch_gemv_decode_norm(md->lm_head, xl, md->final_norm, c.norm_eps, md->logits, s)) != RQ_OK)
+        return st;
+    hipLaunchKernelGGL(k_set_position, dim3(1), dim3(1), 0, s, md->pos, md->n_prompt, p0 + n - 1, p0 + n);
+    RQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(AT), 0, s, md->logits, c.vocab, md->embed, H, md->tokens, md->pos,
+                       md->n_prompt, md->x);
+    RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 
@@ -563,6 +626,10 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(part_floats * 4) + pad(2 * I * 2) +
              2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4) +
              pad((size_t)c.max_seq * (c.head_dim / 2) * sizeof(float2));
+    // batched prompt buffers: up to kPrefillRows positions per chunk
+    const int cap = (int)std::min<int64_t>(((int64_t)c.max_seq + 31) / 32 * 32, kPrefillRows);
+    bytes += 2 * pad((size_t)cap * H * 4) + pad((size_t)cap * QKV * 4) + pad((size_t)cap * H * 2) +
+             2 * pad((size_t)cap * QW * 2) + pad((size_t)2 * cap * I * 2);
     hipError_t e = hipMalloc(&md->owned, bytes);
     if (e != hipSuccess) {
         md->owned = nullptr;
@@ -614,6 +681,14 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     md->pos = carve<int>(p, 1);
     md->n_prompt = carve<int>(p, 1);
     md->rope = carve<float2>(p, (size_t)c.max_seq * (c.head_dim / 2));
+    md->px = carve<float>(p, (size_t)cap * H);
+    md->py = carve<float>(p, (size_t)cap * H);
+    md->pqkv = carve<float>(p, (size_t)cap * QKV);
+    md->pxn = carve<_Float16>(p, (size_t)cap * H);
+    md->pq = carve<_Float16>(p, (size_t)cap * QW);
+    md->patt = carve<_Float16>(p, (size_t)cap * QW);
+    md->ph = carve<_Float16>(p, (size_t)2 * cap * I);
+    md->prefill_cap = md->prefill_rows = cap;
 
     {
         const int64_t n = (int64_t)c.max_seq * (c.head_dim / 2);
@@ -675,11 +750,18 @@ int rq_llama_prefill(rq_llama *md, const int32_t *tokens, int32_t n, rq_stream s
     hipStream_t s = pick(md->ctx, stream);
     RQ_HIP_TRY(hipMemcpyAsync(md->tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
     RQ_HIP_TRY(hipStreamSynchronize(s));  // the host array may be released on return
-    hipLaunchKernelGGL(k_embed_start, dim3(1), dim3(NT), 0, s, md->tokens, md->embed, md->cfg.hidden, md->x, md->pos,
-                       md->n_prompt, n);
-    RQ_LAUNCH_CHECK();
     int st;
-    if ((st = run_steps(md, n, s)) != RQ_OK) return st;
+    if (md->prefill_rows > 0) {
+        for (int p0 = 0; p0 < n; p0 += md->prefill_rows) {
+            const int rows = std::min(md->prefill_rows, n - p0);
+            if ((st = prefill_chunk(md, p0, rows, p0 + rows == n, s)) != RQ_OK) return st;
+        }
+    } else {
+        hipLaunchKernelGGL(k_embed_start, dim3(1), dim3(NT), 0, s, md->tokens, md->embed, md->cfg.hidden, md->x,
+                           md->pos, md->n_prompt, n);
+        RQ_LAUNCH_CHECK();
+        if ((st = run_steps(md, n, s)) != RQ_OK) return st;
+    }
     md->host_pos = n;
     md->host_len = n + 1;
     return RQ_OK;
@@ -704,6 +786,15 @@ int rq_llama_set_graph(rq_llama *md, int use_graph) {
     if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
     RQ_ENTER(md->ctx);
     md->use_graph = use_graph != 0;
+    return RQ_OK;
+}
+
+int rq_llama_set_prefill(rq_llama *md, int32_t rows) {
+    if (!md) return fail(RQ_ERR_INVALID_ARGUMENT, "null runner");
+    RQ_ENTER(md->ctx);
+    if (rows < 0 || rows % 32 != 0 || rows > md->prefill_cap)
+        return fail(RQ_ERR_SHAPE, "prefill chunk of %d rows: 0 or a multiple of 32 up to %d", rows, md->prefill_cap);
+    md->prefill_rows = rows;
     return RQ_OK;
 }
 

@@ -12,8 +12,9 @@ tokens.
 
 The reference has no decode loop (its LlamaModel::forward takes the ids and a
 KV cache but nothing drives generation); the loop defined here is: prefill the
-prompt one position at a time (teacher forcing), then each decode step feeds
-the previous greedy token.
+prompt -- every position of a chunk at once (GEMMs over the chunk's rows and a
+causal prefill attention), or one position at a time through the decode step
+(``set_prefill(0)``) -- then each decode step feeds the previous greedy token.
 """
 from __future__ import annotations
 
@@ -250,6 +251,11 @@ class LlamaRunner:
     def set_graph(self, use_graph: bool) -> None:
         """Graph launch per step (default) or direct kernel launches."""
         call("rq_llama_set_graph", self.handle, int(bool(use_graph)))
+
+    def set_prefill(self, rows: int) -> None:
+        """Positions per batched prompt chunk (a multiple of 32), or 0 for one
+        position at a time through the decode step."""
+        call("rq_llama_set_prefill", self.handle, int(rows))
 
     def tokens(self, stream=None) -> np.ndarray:
         n = ctypes.c_int32()

@@ -114,6 +114,32 @@ def test_mixed_qkv_formats_refused(ctx):
         LlamaRunner(ctx, TINY, w)
 
 
+@pytest.mark.parametrize("cfg", [
+    TINY,
+    LlamaConfig(n_layers=2, hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, intermediate=384, vocab=500,
+                max_seq=160),
+], ids=["hd64", "hd128"])
+def test_prefill_chunks_and_stepwise(ctx, cfg):
+    """The prompt through the batched prefill in one chunk (the default), in
+    chunks of 32 positions (the later chunks attend to the cache the earlier
+    ones wrote) and one position at a time through the decode step: each
+    against the oracle, for the prompt's last logits and up to 8 decode steps."""
+    w = synth_weights(cfg, seed=cfg.hidden + 7)
+    prompt = np.random.default_rng(41).integers(0, cfg.vocab, 90)
+    r = LlamaRunner(ctx, cfg, w)
+    for rows in (None, 32, 64, 0):
+        if rows is not None:
+            r.set_prefill(rows)
+        toks, logits = run_collect(r, prompt, min(8, cfg.max_seq - 90))
+        np.testing.assert_array_equal(toks[:90], prompt)
+        check_steps(cfg, w, toks, logits, 90, 1e-2, f"prefill rows={rows} hd={cfg.head_dim}")
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        r.set_prefill(33)
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        r.set_prefill(((cfg.max_seq + 31) // 32 + 1) * 32)
+    r.close()
+
+
 def test_restart_and_single_token_prompt(ctx):
     w = synth_weights(TINY, seed=21)
     r = LlamaRunner(ctx, TINY, w)
@@ -152,8 +178,9 @@ def test_invalid_arguments(ctx):
 
 
 def test_llama_1b_128_greedy_steps(ctx):
-    """1.1B shape, 512-token prompt, 128 greedy decode steps; every
-    generated token and the last step's logits checked against the oracle."""
+    """1.1B shape, 512-token prompt (one batched prefill chunk), 128
+    greedy decode steps; every generated token, the prompt's last logits and the
+    last step's logits checked against the oracle."""
     cfg = LLAMA_1B
     w = synth_weights(cfg, seed=0)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, 512)
