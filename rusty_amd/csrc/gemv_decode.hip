@@ -496,6 +496,23 @@ Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int s
 
 }  // namespace
 
+// The kernel instance for a supported call and the weight rows each of its
+// blocks covers (block j: rows j * rows ..).
+static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, int *rows) {
+    const int64_t N = w.n_out, K = w.k_in;
+    const int C = (int)(K / 16);
+    const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
+    const int cpt = (int)cdiv(C, tpr);
+    const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
+    const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
+    const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0)
+                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0);
+    *rows = d.r * (DT / tpr);
+    return d;
+}
+
 // x: fp16 activations, or (nw != null, m = 1) the f32 row to RMS-normalise
 // with the fp16 weight nw and epsilon eps, or (sa > 0, m = 1) the attention
 // partials to combine (sa per head of attn_hd elements).
@@ -511,18 +528,9 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     if (sa && (m != 1 || w2 || nw || (sa != 1 && sa != 2 && sa != 4 && sa != 8) || attn_hd < 8 ||
                attn_hd % 8 != 0 || K % attn_hd != 0))
         return RQ_ERR_UNSUPPORTED;
-    const int C = (int)(K / 16);
-    const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
-    const int cpt = (int)cdiv(C, tpr);
-    const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
-    const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
-    const bool swi = w2 != nullptr, norm = nw != nullptr;
-    const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0)
-                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0);
-    const bool fx = norm || sa;  // x is an f32 source read by the prologue
-    const int rows = d.r * (DT / tpr);
+    int rows;
+    const Decode d = plan(w, w2 != nullptr, nw != nullptr, m, sa, &rows);
+    const bool fx = nw || sa;  // x is an f32 source read by the prologue
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
                        w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, w2 ? w2->biases : nullptr,
