@@ -462,6 +462,45 @@ def cpu_baseline(seconds: float):
                        f"bytes counted as the int8 algorithmic bytes of the GPU step")}
 
 
+def vendor_gemm(reps: int = 5) -> list:
+    """Comparison only: the vendor's fp16 GEMM (torch.matmul, hipBLASLt on this
+    image) on the prefill shapes with random fp16 operands and no dequantization,
+    Y = X . W^T, 40 launches over 8 weight copies per captured graph, HIP events
+    around the graph replay, best of `reps`."""
+    import torch
+
+    out = []
+    g0 = torch.Generator(device="cuda").manual_seed(0)
+    for m, n, k in ((2048, 4096, 4096), (2048, 11008, 4096), (2048, 4096, 11008), (512, 4096, 4096)):
+        a = torch.randn(m, k, device="cuda", dtype=torch.float16, generator=g0)
+        ws = [torch.randn(n, k, device="cuda", dtype=torch.float16, generator=g0) for _ in range(8)]
+        for _ in range(50):
+            a @ ws[0].T
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(40):
+                a @ ws[i % 8].T
+        graph.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(reps):
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            graph.replay()
+            t1.record()
+            t1.synchronize()
+            ms = t0.elapsed_time(t1) / 40
+            best = ms if best is None else min(best, ms)
+        tf = 2 * m * n * k / (best * 1e-3) / 1e12
+        out.append({"shape": f"{m}x{n}x{k}", "us": round(best * 1e3, 1), "tflops": round(tf, 1),
+                    "frac_of_fp16_peak": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+                    "library": str(torch.backends.cuda.preferred_blas_library())})
+        log(f"vendor fp16 GEMM {out[-1]}")
+        del a, ws, graph
+    return out
+
+
 def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
     """configs[1] at M = 4, 16 and the SwiGLU-shaped GEMVs at M = 1, 8, each
     over enough rotating weight copies to stay out of the Infinity Cache."""
@@ -495,7 +534,7 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor", "vendor"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
@@ -529,6 +568,8 @@ def main() -> int:
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
         elif args.only == "swiglu":
             out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
+        elif args.only == "vendor":
+            out["vendor_gemm"] = vendor_gemm()
         else:
             out["decode"] = decode_loop(ctx, eager=args.decode_eager)
         log(f"{out}")
