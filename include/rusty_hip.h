@@ -186,6 +186,22 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
 int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, void *y,
                rq_dtype y_dtype, int64_t m, rq_stream stream);
 
+/* Linear::forward with a LoRA adapter (rusty-graph/src/lib.rs:69-83; the
+ * adapter's tensors LoRAAdapter, lib.rs:17-22):
+ *   Y[m, n_out] = X . deq(W)^T + (X . A) . B,
+ * A f32 [k_in, rank], B f32 [rank, n_out] (row-major), added unscaled as the
+ * reference does.  The adapter's products are f32 with one fma accumulator
+ * per output over k ascending, then one f32 add to the fused product (which
+ * is computed in f32); Y is rounded to y_dtype once.  rank 0 adds nothing.
+ * workspace: device memory of at least rq_qmatmul_lora_workspace(...) bytes
+ * (f32 copies of X when it is fp16, X.A, (X.A).B, and the fused product when
+ * Y is fp16).  Uses the context's GEMM workspace as rq_qmatmul does. */
+size_t rq_qmatmul_lora_workspace(int64_t m, int64_t k_in, int64_t n_out, int64_t rank, rq_dtype x_dtype,
+                                 rq_dtype y_dtype);
+int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, const float *lora_a,
+                    const float *lora_b, int64_t rank, void *y, rq_dtype y_dtype, int64_t m, void *workspace,
+                    size_t workspace_bytes, rq_stream stream);
+
 /* MLP::forward (rusty-graph/src/lib.rs:317-323):
  * y = down( silu(x . gate^T) * (x . up^T) ), silu(v) = v / (1 + exp(-v))
  * (kernels.wgsl:104-113; the elementwise product kernels.wgsl:146-151).

@@ -115,12 +115,15 @@ _SIGNATURES = {
     "rq_llama_destroy": [_P],
     "rq_llama_prefill": [_P, POINTER(c_int32), c_int32, _P],
     "rq_llama_decode": [_P, c_int32, _P],
+    "rq_qmatmul_lora_workspace": [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int],
+    "rq_qmatmul_lora": [_P, POINTER(rq_qweight), _P, c_int, _P, _P, ctypes.c_int64, _P, c_int, ctypes.c_int64, _P,
+                        c_size_t, _P],
     "rq_llama_set_graph": [_P, c_int],
     "rq_llama_set_prefill": [_P, c_int32],
     "rq_llama_tokens": [_P, POINTER(c_int32), c_int32, POINTER(c_int32), _P],
     "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }
-_RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p}
+_RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p, "rq_qmatmul_lora_workspace": c_size_t}
 
 
 class RqError(RuntimeError):

@@ -1,0 +1,109 @@
+// Linear::forward with a LoRA adapter (rusty-graph/src/lib.rs:69-83):
+//   out = x . W + (x . A) . B,   A [in, rank], B [rank, out] (LoRAAdapter,
+//   lib.rs:17-22), added unscaled as the reference does (its alpha is unused).
+// Here W is the quantized [out, in] weight, so the first term is rq_qmatmul's
+// fused dequant product.  The adapter's two products keep the reference's
+// arithmetic: f32 operands, one fma accumulator per output over k ascending
+// (the f32 matmul kernel, matmul_f32.hip), then one f32 add per output --
+// so with W's term exactly zero the result equals the reference's f32 path
+// bit for bit.  Launches: [x widened to f32], t = x . A, l = t . B, the fused
+// product into f32, y = main + l (rounded to y's dtype).  The adapter's work
+// is (m . in + m . out) . rank fmas and m . (rank + 2 out) floats of traffic:
+// small next to the weight for the ranks adapters use (<= 64).
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace rq {
+namespace {
+
+constexpr int TH = 256;
+
+__global__ __launch_bounds__(TH) void k_widen_f16(const _Float16 *__restrict__ x, float *__restrict__ out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * TH + threadIdx.x; i < n; i += (int64_t)gridDim.x * TH)
+        out[i] = (float)x[i];
+}
+
+// y = main + l; main may alias y when y is f32.
+template <bool F16>
+__global__ __launch_bounds__(TH) void k_lora_add(const float *main, const float *__restrict__ l, void *y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * TH + threadIdx.x; i < n; i += (int64_t)gridDim.x * TH) {
+        const float v = main[i] + l[i];
+        if constexpr (F16) static_cast<_Float16 *>(y)[i] = (_Float16)v;
+        else static_cast<float *>(y)[i] = v;
+    }
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, TH), 16384)); }
+
+}  // namespace
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" {
+
+size_t rq_qmatmul_lora_workspace(int64_t m, int64_t k_in, int64_t n_out, int64_t rank, rq_dtype x_dtype,
+                                 rq_dtype y_dtype) {
+    if (m < 0 || k_in < 0 || n_out < 0 || rank < 0) return 0;
+    const int64_t floats = (x_dtype == RQ_F16 ? m * k_in : 0) + m * rank + m * n_out +
+                           (y_dtype == RQ_F16 ? m * n_out : 0);
+    return (size_t)floats * 4 + 4 * 256;  // + alignment of each part to 256 bytes
+}
+
+int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, const float *lora_a,
+                    const float *lora_b, int64_t rank, void *y, rq_dtype y_dtype, int64_t m, void *workspace,
+                    size_t workspace_bytes, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    if ((x_dtype != RQ_F16 && x_dtype != RQ_F32) || (y_dtype != RQ_F16 && y_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    if (m < 0 || rank < 0) return fail(RQ_ERR_SHAPE, "negative m or rank");
+    const int64_t K = w->k_in, N = w->n_out;
+    int64_t t;
+    if (!mul_ok(m, K, &t) || !mul_ok(m, N, &t) || !mul_ok(m, rank, &t) || !mul_ok(rank, N, &t) ||
+        !mul_ok(rank, K, &t))
+        return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0 || N == 0) return RQ_OK;
+    if (!y || (K > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
+    if (rank > 0 && (!lora_a || !lora_b)) return fail(RQ_ERR_INVALID_ARGUMENT, "null adapter pointer");
+    const size_t need = rq_qmatmul_lora_workspace(m, K, N, rank, x_dtype, y_dtype);
+    if (!workspace || workspace_bytes < need)
+        return fail(RQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    hipStream_t s = pick(ctx, stream);
+    // carve the workspace: [x f32][t][l][main f32]
+    char *p = static_cast<char *>(workspace);
+    auto carve = [&p](int64_t floats) {
+        p = reinterpret_cast<char *>((reinterpret_cast<uintptr_t>(p) + 255) & ~uintptr_t(255));
+        float *r = reinterpret_cast<float *>(p);
+        p += floats * 4;
+        return r;
+    };
+    const float *xf = static_cast<const float *>(x);
+    if (x_dtype == RQ_F16) {
+        float *w32 = carve(m * K);
+        if (m * K > 0) {
+            hipLaunchKernelGGL(k_widen_f16, dim3(grid_for(m * K)), dim3(TH), 0, s, static_cast<const _Float16 *>(x),
+                               w32, m * K);
+            RQ_LAUNCH_CHECK();
+        }
+        xf = w32;
+    }
+    float *tv = carve(m * rank);
+    float *lv = carve(m * N);
+    float *mainv = y_dtype == RQ_F16 ? carve(m * N) : static_cast<float *>(y);
+    // t = x . A [m, rank], l = t . B [m, n_out]: one fma chain per output, k ascending
+    if ((st = launch_matmul_f32(MM_AB, xf, lora_a, tv, m, K, rank, s)) != RQ_OK) return st;
+    if ((st = launch_matmul_f32(MM_AB, tv, lora_b, lv, m, rank, N, s)) != RQ_OK) return st;
+    // the fused dequant product, f32
+    if ((st = qmatmul_dispatch(ctx, *w, x, x_dtype, mainv, RQ_F32, m, s)) != RQ_OK) return st;
+    if (y_dtype == RQ_F16)
+        hipLaunchKernelGGL(k_lora_add<true>, dim3(grid_for(m * N)), dim3(TH), 0, s, mainv, lv, y, m * N);
+    else
+        hipLaunchKernelGGL(k_lora_add<false>, dim3(grid_for(m * N)), dim3(TH), 0, s, mainv, lv, y, m * N);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+}  // extern "C"

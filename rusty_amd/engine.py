@@ -302,6 +302,29 @@ class ComputeEngine:
         call("rq_qmatmul", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], out.ptr, _XDT[out.dtype], m,
              _stream(stream))
 
+    def qmatmul_lora(self, ctx: WgpuContext, x: UnifiedTensor, w: QuantizedTensor, lora_a: UnifiedTensor,
+                     lora_b: UnifiedTensor, out: UnifiedTensor, workspace: UnifiedTensor | None = None,
+                     stream=None) -> None:
+        """``Linear::forward`` with a LoRA adapter (rusty-graph/src/lib.rs:69-83):
+        ``out = x . deq(w)^T + (x . A) . B``, A f32 [k_in, rank], B f32
+        [rank, n_out], unscaled as the reference adds it."""
+        if x.dtype not in _XDT or out.dtype not in _XDT:
+            raise ValueError("x and out must be FP16 or FP32")
+        if lora_a.dtype is not DType.FP32 or lora_b.dtype is not DType.FP32:
+            raise ValueError("the adapter's A and B must be FP32")
+        m = x.numel // w.k_in if w.k_in else x.shape[0]
+        rank = lora_a.numel // w.k_in if w.k_in else 0
+        if x.numel != m * w.k_in or out.numel != m * w.n_out or lora_a.numel != w.k_in * rank \
+                or lora_b.numel != rank * w.n_out:
+            raise ValueError(f"x {x.shape} / A {lora_a.shape} / B {lora_b.shape} / out {out.shape} do not match "
+                             f"weight [{w.n_out}, {w.k_in}]")
+        need = _lib.lib().rq_qmatmul_lora_workspace(m, w.k_in, w.n_out, rank, _XDT[x.dtype], _XDT[out.dtype])
+        if workspace is None:
+            workspace = UnifiedTensor.empty(ctx, [max(need, 1)], DType.U8)
+        d = w.descriptor()
+        call("rq_qmatmul_lora", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], lora_a.ptr, lora_b.ptr, rank,
+             out.ptr, _XDT[out.dtype], m, workspace.ptr, workspace.numel * workspace.dtype.itemsize, _stream(stream))
+
     def qmatmul_dx(self, ctx: WgpuContext, dy: UnifiedTensor, w: QuantizedTensor, dx: UnifiedTensor,
                    stream=None) -> None:
         """Input gradient of ``qmatmul`` with the weight frozen:
