@@ -1,9 +1,9 @@
 """GPU parity of the quantized-weight Llama decode runner (rq_llama_*) against the oracle.
 
-The device runs the sequence one position at a time through its KV cache
-(one graph launch per token); the oracle (oracle/llama.py) runs the whole
-sequence at once in float64 with causal attention, teacher-forced on the
-device's tokens.  Checks per step:
+The device runs the prompt through its batched prefill (or one position at a
+time, set_prefill(0)), then one graph launch per generated token; the oracle
+(oracle/llama.py) runs the whole sequence at once in float64 with causal
+attention, teacher-forced on the device's tokens.  Checks per step:
   * logits: max|d| <= TOL * max|logits_ref| for that step;
   * greedy: the device's token has a reference logit within
     2 * TOL * max|logits_ref| of the reference maximum (a near tie may pick
@@ -179,30 +179,18 @@ def test_invalid_arguments(ctx):
 
 def test_llama_1b_128_greedy_steps(ctx):
     """1.1B shape, 512-token prompt (one batched prefill chunk), 128
-    greedy decode steps; every generated token, the prompt's last logits and the
-    last step's logits checked against the oracle."""
+    greedy decode steps; the logits of every step (the prompt's last position,
+    then each generated one) and every generated token checked against the
+    oracle, teacher-forced on the device's tokens."""
     cfg = LLAMA_1B
     w = synth_weights(cfg, seed=0)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, 512)
     r = LlamaRunner(ctx, cfg, w)
-    r.prefill(prompt)
-    first = r.logits()
-    r.decode(127)
-    last = r.logits()
-    toks = r.tokens()
-    assert toks.shape == (640,)
+    toks, logits = run_collect(r, prompt, 127)
     r.close()
-    ref = ol.forward(cfg, w, toks[:639], first=511)  # positions 511..638
-    tol = 2e-2
-    worst = 0.0
-    for i in range(ref.shape[0]):
-        scale = np.abs(ref[i]).max()
-        assert ref[i][toks[512 + i]] >= ref[i].max() - 2 * tol * scale, f"step {i}: token {toks[512 + i]}"
-    for i, dev in ((0, first), (127, last)):
-        d = np.abs(dev - ref[i]).max() / np.abs(ref[i]).max()
-        worst = max(worst, d)
-        assert d <= tol, f"step {i}: logits rel diff {d:.3e}"
-    print(f"[1B] 128 greedy tokens consistent; logits rel diff (first, last) <= {worst:.3e}", flush=True)
+    assert toks.shape == (640,) and logits.shape == (128, cfg.vocab)
+    np.testing.assert_array_equal(toks[:512], prompt)
+    check_steps(cfg, w, toks, logits, 512, 2e-2, "1B")
 
 
 @pytest.mark.parametrize("cfg,n_prompt", [
