@@ -25,7 +25,8 @@
 // for lane half h); V^T is staged in LDS per key tile (each lane loads 4 keys
 // x 8 dims and writes 8 four-key pieces), and each lane reads its two 8-byte
 // pieces of a row of V^T in that key order.  Scores, softmax and the
-// accumulators are f32; q, k, v and p enter the matrix cores as fp16.
+// accumulators are f32 (exponentials as 2^x on scores scaled by log2 e);
+// q, k, v and p enter the matrix cores as fp16.
 #include "common.hpp"
 
 namespace rq {
@@ -191,7 +192,9 @@ __global__ __launch_bounds__(NW * 64) void k_attn_prefill(const _Float16 *__rest
     const int last = min(p0 + q0 + 31, kv_len - 1);  // the tile's last live query
     const int ntiles = last / 32 + 1;
     const int iters = (ntiles + NW - 1) / NW;  // the same for every wave (barriers below)
-    const float scale = 1.0f / sqrtf((float)HD);
+    // scores are kept in log2 units, (q.k / sqrt(HD)) * log2(e), so every
+    // exponential is one v_exp_f32 (2^x); the softmax is unchanged
+    const float scale = 1.4426950408889634f / sqrtf((float)HD);
     float m_run = -__builtin_inff(), l_run = 0.0f;
     floatx16 o[DT];
 #pragma unroll
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_prefill(const _Float16 *__rest
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             const float m_new = fmaxf(m_run, mt);
-            const float alpha = expf(m_run - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -246,7 +249,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_prefill(const _Float16 *__rest
                 for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = expf(sc[r] - m_new);
+                const float p = __builtin_amdgcn_exp2f(sc[r] - m_new);
                 l_run += p;
                 pf[r >> 3][r & 7] = (_Float16)p;
             }
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_prefill(const _Float16 *__rest
     float wt[NW], L = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        wt[w] = expf(cm[w][lane] - mx);
+        wt[w] = __builtin_amdgcn_exp2f(cm[w][lane] - mx);
         L = fmaf(wt[w], cl[w][lane] + cl[w][lane ^ 32], L);  // both halves of the query's keys
     }
     const float inv = 1.0f / L;
