@@ -19,8 +19,9 @@ Printed JSON (one line, stdout):
                    f32 GEMV on the load-time-dequantized f32 weight (oracle port)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
   prefill_mid      the same GEMM at M=256 and 512 (4096x4096), not a configs[] shape
-  decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2]), and
-                   the reference's affine format (u8 codes, scale+bias per 64)
+  decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2]), the
+                   reference's affine format (u8 codes, scale+bias per 64), and
+                   f32 activations (the reference's dtype) at M=1/4/16
   prefill_affine   the dequant-GEMM on affine weights, fp16 and f32 activations
   swiglu           configs[2]: the fused SwiGLU MLP (gate+up pass, then down)
                    at the 7B shape, M=1 and M=8, GB/s of its algorithmic bytes
@@ -61,7 +62,8 @@ class GemvWorkload:
     codes with one f32 scale per row (the configs), or with `affine` the
     reference's format: u8 codes with an f32 scale and bias per 64 elements."""
 
-    def __init__(self, ctx, m: int, n: int, k: int, seed: int = 0, copies: int = COPIES, affine: bool = False):
+    def __init__(self, ctx, m: int, n: int, k: int, seed: int = 0, copies: int = COPIES, affine: bool = False,
+                 x_f32: bool = False):
         from rusty_amd import DType, UnifiedTensor, _lib, synth
 
         self.ctx, self.m, self.n, self.k, self.copies = ctx, m, n, k, copies
@@ -84,7 +86,9 @@ class GemvWorkload:
             if affine:
                 _lib.call("rq_memcpy_d2d", ctx.handle, self.biases.ptr + c * ns * 4, fb.ptr, ns * 4, None)
         ctx.sync()
-        self.x = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+        self.x_dtype = 0 if x_f32 else 1  # RQ_F32 / RQ_F16: f32 is the reference's activation dtype
+        self.x = UnifiedTensor.new(ctx, x.astype(np.float32), dtype=DType.FP32) if x_f32 else \
+            UnifiedTensor.new(ctx, x, dtype=DType.FP16)
         self.y = UnifiedTensor.empty(ctx, [m, n], DType.FP16)
         fmt = _lib.RQ_Q_AFFINE_U8 if affine else _lib.RQ_Q_ROWWISE_I8
         self.desc = [_lib.rq_qweight(self.codes.ptr + c * n * k, self.scales.ptr + c * ns * 4,
@@ -92,10 +96,11 @@ class GemvWorkload:
                      for c in range(copies)]
         self._fn = _lib.lib().rq_qmatmul
         self._h = ctx.handle
-        self.bytes = gemv_bytes(m, n, k) + (4 * n * k // 64 * 2 - 4 * n if affine else 0)
+        self.bytes = gemv_bytes(m, n, k) + (4 * n * k // 64 * 2 - 4 * n if affine else 0) + (2 * m * k if x_f32 else 0)
 
     def launch(self, i: int) -> None:
-        st = self._fn(self._h, ctypes.byref(self.desc[i % self.copies]), self.x.ptr, 1, self.y.ptr, 1, self.m, None)
+        st = self._fn(self._h, ctypes.byref(self.desc[i % self.copies]), self.x.ptr, self.x_dtype, self.y.ptr, 1,
+                      self.m, None)
         if st != 0:
             from rusty_amd import _lib
             _lib.check(st, "rq_qmatmul")
@@ -505,18 +510,23 @@ def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
     """configs[1] at M = 4, 16 and the SwiGLU-shaped GEMVs at M = 1, 8, each
     over enough rotating weight copies to stay out of the Infinity Cache."""
     extra = {}
-    for m, n, k, aff in ((4, 4096, 4096, False), (16, 4096, 4096, False), (1, 11008, 4096, False),
-                         (8, 11008, 4096, False), (1, 4096, 11008, False), (8, 4096, 11008, False),
-                         (1, 4096, 4096, True), (4, 4096, 4096, True), (16, 4096, 4096, True)):
+    for m, n, k, aff, xf in ((4, 4096, 4096, False, False), (16, 4096, 4096, False, False),
+                             (1, 11008, 4096, False, False), (8, 11008, 4096, False, False),
+                             (1, 4096, 11008, False, False), (8, 4096, 11008, False, False),
+                             (1, 4096, 4096, True, False), (4, 4096, 4096, True, False),
+                             (16, 4096, 4096, True, False), (1, 4096, 4096, False, True),
+                             (4, 4096, 4096, False, True), (16, 4096, 4096, False, True)):
         copies = max(2, min(COPIES, (1200 << 20) // (n * k)))
-        w2 = GemvWorkload(ctx, m, n, k, copies=copies, affine=aff)
+        w2 = GemvWorkload(ctx, m, n, k, copies=copies, affine=aff, x_f32=xf)
         wms, _ = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
         kms = wms / (20 * copies)
-        key = f"m{m}_{n}x{k}" + ("_affine" if aff else "")
+        key = f"m{m}_{n}x{k}" + ("_affine" if aff else "") + ("_x_f32" if xf else "")
         extra[key] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1), "us_per_launch": round(kms * 1e3, 2),
                       "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": w2.bytes}
         if aff:
             extra[key]["weights"] = "affine u8, f32 scale+bias per 64 (the reference's format)"
+        if xf:
+            extra[key]["activations"] = "f32 (the reference's dtype), kept to f32 accuracy"
         log(f"GEMV {key}: {extra[key]}")
         del w2
     return extra

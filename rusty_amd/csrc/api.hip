@@ -444,9 +444,10 @@ int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dty
         // kernel also serves the 3-4 token shapes the MFMA kernel refuses
         // (affine codes).
         int st = RQ_ERR_UNSUPPORTED;
-        if (m <= 2 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
-        if (st == RQ_ERR_UNSUPPORTED && m <= 16 && xt == RQ_F16) st = launch_gemv_mfma(w, x, y, yt, (int)m, s);
-        if (st == RQ_ERR_UNSUPPORTED && m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, y, yt, (int)m, s);
+        // f32 activations take the same kernels, rounded to fp16 as they load
+        if (m <= 2) st = launch_gemv_decode(w, x, xt, y, yt, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 16) st = launch_gemv_mfma(w, x, xt, y, yt, (int)m, s);
+        if (st == RQ_ERR_UNSUPPORTED && m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, xt, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(w, x, xt, y, yt, (int)m, ctx->num_cus, s);
         if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, gemm_workspace(ctx, s), s);
         if (st != RQ_ERR_UNSUPPORTED) return st;
@@ -482,9 +483,10 @@ int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, co
                    hipStream_t s) {
     const int64_t I = gate.n_out;
     int st = RQ_ERR_UNSUPPORTED;
-    if (x_dtype == RQ_F16 && m <= 2) st = launch_swiglu_decode(gate, up, x, h, (int)m, s);
-    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 16) st = launch_swiglu_mfma(gate, up, x, h, (int)m, s);
-    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4) st = launch_swiglu_decode(gate, up, x, h, (int)m, s);
+    if (m <= 2) st = launch_swiglu_decode(gate, up, x, x_dtype, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && m <= 16) st = launch_swiglu_mfma(gate, up, x, x_dtype, h, (int)m, s);
+    if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4)
+        st = launch_swiglu_decode(gate, up, x, x_dtype, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && m > 16) {
         // prefill: gate and up through the GEMM into the two halves of the
         // workspace, then h = silu(g) * u in place over the first half

@@ -67,7 +67,7 @@ int launch_rowwise_dequantize(const int8_t *q, const float *scales, float *out, 
                               int64_t k, hipStream_t s);
 int launch_matmul_f32(int variant, const float *a, const float *b, float *out, int64_t m, int64_t k,
                       int64_t n, hipStream_t s);
-int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
+int launch_gemv_decode(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m, hipStream_t s);
 // m = 1..4 decode GEMV that adds its result into an f32 y (y += X . deq(W)^T):
 // the residual connection fused into the projection's epilogue.
 int launch_gemv_decode_add(const rq_qweight &w, const void *x, float *y, int m, hipStream_t s);
@@ -75,7 +75,7 @@ int launch_gemv_decode_add(const rq_qweight &w, const void *x, float *y, int m, 
 // kernel's prologue from the f32 row x (no separate norm launch); f32 y.
 int launch_gemv_decode_norm(const rq_qweight &w, const float *x, const _Float16 *nw, float eps, float *y,
                             hipStream_t s);
-int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s);
+int launch_gemv_mfma(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m, hipStream_t s);
 int launch_gemv(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m,
                 int num_cus, hipStream_t s);
 // Split-K workspace of the prefill GEMM: kGemmSkFloats f32 partial sums and
@@ -101,7 +101,8 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
                 const GemmWorkspace &ws, hipStream_t s);
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                            int64_t m, hipStream_t s);
-int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
+int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,
+                         hipStream_t s);
 // SwiGLU gate/up pass over RMSNorm(x) . nw (m = 1, f32 x), h fp16.
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
                               float eps, void *h, hipStream_t s);
@@ -111,7 +112,8 @@ int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, cons
 // (m, l)[head][n_split] float2.
 int launch_gemv_decode_attn_add(const rq_qweight &w, const float *partials, int n_split, int head_dim, float *y,
                                 hipStream_t s);
-int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s);
+int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,
+                       hipStream_t s);
 int launch_swiglu_generic(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h,
                           int64_t m, hipStream_t s);
 int launch_silu_mul(const void *g, const void *u, void *h, int64_t n, hipStream_t s);

@@ -1,4 +1,5 @@
-// Decode dequant-GEMV, fp16 activations, m <= 4:  Y[m, n] = sum_k X[m, k] * deq(W)[n, k].
+// Decode dequant-GEMV, m <= 4:  Y[m, n] = sum_k X[m, k] * deq(W)[n, k], fp16
+// activations (f32 ones, m <= 2, rounded to fp16 as they are loaded).
 // Serves m = 1-2, and m = 3-4 for the weights the MFMA GEMV does not take
 // (affine codes); per-row codes at m >= 3 go to the MFMA GEMV.
 //
@@ -89,7 +90,9 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // split over positions): Xf holds acc[head][SA][attn_hd] (f32) followed by
 // (m, l)[head][SA] (float2); x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
 // M = max_s m_s, rounded to fp16 and shared through LDS like the norm's row.
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0>
+// XF (no NORM / SA): the activations are f32 (Xf), rounded to fp16 as they
+// are loaded.
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
                                                     const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
@@ -100,6 +103,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                                                     int group, int attn_hd) {
     static_assert(!NORM || M == 1, "the fused norm serves one activation row");
     static_assert(SA == 0 || (M == 1 && !NORM && !SWI), "the attention combine serves one activation row");
+    static_assert(!XF || (!NORM && SA == 0), "f32 activations replace the plain fp16 row");
     constexpr int RP = DT / TPR;
     constexpr int ROWS = R * RP;
     constexpr int TASKS = ROWS * M;
@@ -118,6 +122,8 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     constexpr int XC = CPT * TPR;            // chunks the row groups cover
     constexpr int NL = (XC + DT - 1) / DT;   // NORM: chunks loaded per thread
     uint32_t xh[CPT][M][8];
+    // XF: x = xh + xl exactly to ~2^-22 relative (xh = fp16(x), xl = fp16(x - xh))
+    uint32_t xl[XF ? CPT : 1][XF ? M : 1][8];
     uint4 xf4[NORM ? NL : 1][4], nw4[NORM ? NL : 1][2];
     // SA: 8-element pieces of the row, piece u by thread u % DT: SA (m, l)
     // pairs of its head and SA x 8 accumulator values
@@ -154,6 +160,33 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             for (int q = 0; q < 4; ++q) xf4[j][q] = bload<0>(rxf, off + 16 * q);
             nw4[j][0] = bload<0>(rnw, offw);
             nw4[j][1] = bload<0>(rnw, offw + 16);
+        }
+    } else if constexpr (XF) {
+        // f32 activations (the reference's dtype): 64 bytes per chunk, each
+        // value split into two fp16 terms in registers
+        const auto rx = make_rsrc(Xf, (uint32_t)m_act * (uint32_t)K * 4u);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tt + TPR * j;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint32_t off = c < C ? ((uint32_t)m * K + (uint32_t)c * 16) * 4u : kOOB;
+                uint4 f4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) f4[q] = bload<0>(rx, off + 16 * q);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float f[4] = {__builtin_bit_cast(float, f4[q].x), __builtin_bit_cast(float, f4[q].y),
+                                        __builtin_bit_cast(float, f4[q].z), __builtin_bit_cast(float, f4[q].w)};
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const h2_t h = {(_Float16)f[2 * e], (_Float16)f[2 * e + 1]};
+                        const h2_t l = {(_Float16)(f[2 * e] - (float)h.x), (_Float16)(f[2 * e + 1] - (float)h.y)};
+                        xh[j][m][2 * q + e] = __builtin_bit_cast(uint32_t, h);
+                        xl[j][m][2 * q + e] = __builtin_bit_cast(uint32_t, l);
+                    }
+                }
+            }
         }
     } else {
         const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
@@ -342,6 +375,10 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) s = dot2(xh[j][m][i], 0x3C003C00u, s);
+            if constexpr (XF) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s = dot2(xl[j][m][i], 0x3C003C00u, s);
+            }
             xs[j][m] = s;
             xs_tot[m] += s;
         }
@@ -360,11 +397,24 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t u = FMT == 0 ? (wd[q] ^ 0x80808080u) : wd[q];
-                const uint32_t lo = magic_lo(u), hi = magic_hi(u);
+                uint32_t lo = magic_lo(u), hi = magic_hi(u);
+                if constexpr (XF) {
+                    // exact code values (q, or u for affine) rather than the
+                    // offset ones: at f32 accuracy the offset's products would
+                    // cancel against the correction term
+                    const h2_t off = FMT == 0 ? (h2_t){(_Float16)1152.0f, (_Float16)1152.0f}
+                                              : (h2_t){(_Float16)1024.0f, (_Float16)1024.0f};
+                    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, lo) - off);
+                    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, hi) - off);
+                }
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     d[m] = dot2(lo, xh[j][m][2 * q], d[m]);
                     d[m] = dot2(hi, xh[j][m][2 * q + 1], d[m]);
+                    if constexpr (XF) {
+                        d[m] = dot2(lo, xl[j][m][2 * q], d[m]);
+                        d[m] = dot2(hi, xl[j][m][2 * q + 1], d[m]);
+                    }
                 }
             }
 #pragma unroll
@@ -373,14 +423,15 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                     p[m] = d[m];
                 } else {
                     const float s = sg[r][j];
+                    const float c = XF ? bg[r][j] : __builtin_fmaf(-1024.0f, s, bg[r][j]);
                     p[m] = __builtin_fmaf(s, d[m], p[m]);
-                    p[m] = __builtin_fmaf(__builtin_fmaf(-1024.0f, s, bg[r][j]), xs[j][m], p[m]);
+                    p[m] = __builtin_fmaf(c, xs[j][m], p[m]);
                 }
             }
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const float v = FMT == 0 ? __builtin_fmaf(-1152.0f, xs_tot[m], p[m]) : p[m];
+            const float v = FMT == 0 && !XF ? __builtin_fmaf(-1152.0f, xs_tot[m], p[m]) : p[m];
             // up rows (r >= R) land TASKS entries after their gate rows
             part[(r / R) * TASKS + ((r % R) * RP + rp) * M + m][tt] = v;
         }
@@ -424,8 +475,8 @@ struct Decode {
     DecodeFn fn;
     int r;
 };
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0>
-constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM, SA>, R}; }
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false>
+constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM, SA, XF>, R}; }
 
 // Rows per row group, measured on MI355X with the weights streamed from HBM:
 //  m = 1:
@@ -445,9 +496,9 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //     fewer, larger blocks).
 // fmt: 0 = per-row int8, 1 = affine u8; swi selects the SwiGLU gate/up
 // pass; norm (m = 1) the fused RMSNorm prologue; sa (m = 1) the attention
-// combine of sa partials per head.
+// combine of sa partials per head; xf (m <= 2, no norm / sa) f32 activations.
 template <int M, int CPT, int TPR, int FMT>
-Decode pick_fmt(bool swi, bool norm, bool tall, int sa) {
+Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf) {
     if constexpr (M == 1) {
         constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
         constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
@@ -456,41 +507,54 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa) {
         if (sa == 2) return inst<1, CPT, TPR, 4, FMT, false, false, 2>();
         if (sa == 4) return inst<1, CPT, TPR, 4, FMT, false, false, 4>();
         if (sa == 8) return inst<1, CPT, TPR, 4, FMT, false, false, 8>();
-        if (swi) return norm ? inst<1, CPT, TPR, RSN, FMT, true, true>() : inst<1, CPT, TPR, 2, FMT, true, false>();
-        if (FMT == 0 && tall)
-            return norm ? inst<1, CPT, TPR, 8, FMT, false, true>() : inst<1, CPT, TPR, 8, FMT, false, false>();
+        if (swi) {
+            if (norm) return inst<1, CPT, TPR, RSN, FMT, true, true>();
+            return xf ? inst<1, CPT, TPR, 2, FMT, true, false, 0, true>() : inst<1, CPT, TPR, 2, FMT, true, false>();
+        }
+        if (FMT == 0 && tall) {
+            if (norm) return inst<1, CPT, TPR, 8, FMT, false, true>();
+            return xf ? inst<1, CPT, TPR, 8, FMT, false, false, 0, true>() : inst<1, CPT, TPR, 8, FMT, false, false>();
+        }
         if (norm) return inst<1, CPT, TPR, RN, FMT, false, true>();
-        return inst<1, CPT, TPR, RP, FMT, false, false>();
+        return xf ? inst<1, CPT, TPR, RP, FMT, false, false, 0, true>() : inst<1, CPT, TPR, RP, FMT, false, false>();
+    } else if constexpr (M == 2) {
+        (void)norm;
+        (void)tall;
+        (void)sa;
+        if (swi) return xf ? inst<2, CPT, TPR, 2, FMT, true, false, 0, true>() : inst<2, CPT, TPR, 2, FMT, true, false>();
+        return xf ? inst<2, CPT, TPR, 4, FMT, false, false, 0, true>() : inst<2, CPT, TPR, 4, FMT, false, false>();
     } else {
         (void)norm;
         (void)tall;
         (void)sa;
+        (void)xf;
         if (swi) return inst<M, CPT, TPR, 2, FMT, true, false>();
         return inst<M, CPT, TPR, 4, FMT, false, false>();
     }
 }
 
 template <int M, int CPT, int TPR>
-Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa) {
-    return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa) : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa);
+Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
+    return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa, xf)
+                    : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa, xf);
 }
 
 template <int M, int CPT>
-Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa) {
+Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
     switch (tpr) {
-    case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa);
-    case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa);
-    default: return pick_swi<M, CPT, 256>(fmt, swi, norm, tall, sa);
+    case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa, xf);
+    case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa, xf);
+    default: return pick_swi<M, CPT, 256>(fmt, swi, norm, tall, sa, xf);
     }
 }
 
 template <int M>
-Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
     switch (cpt) {
-    case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa);
-    case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa);
-    case 3: return pick_tpr<M, 3>(tpr, fmt, swi, norm, tall, sa);
-    default: return pick_tpr<M, 4>(tpr, fmt, swi, norm, tall, sa);
+    case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa, xf);
+    case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa, xf);
+    case 3: return pick_tpr<M, 3>(tpr, fmt, swi, norm, tall, sa, xf);
+    default: return pick_tpr<M, 4>(tpr, fmt, swi, norm, tall, sa, xf);
     }
 }
 
@@ -498,7 +562,7 @@ Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int s
 
 // The kernel instance for a supported call and the weight rows each of its
 // blocks covers (block j: rows j * rows ..).
-static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, int *rows) {
+static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool xf, int *rows) {
     const int64_t N = w.n_out, K = w.k_in;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
@@ -506,9 +570,9 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, int 
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
     const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
     const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0)
-                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0);
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa, xf)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xf)
+                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0, false);
     *rows = d.r * (DT / tpr);
     return d;
 }
@@ -517,8 +581,10 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, int 
 // with the fp16 weight nw and epsilon eps, or (sa > 0, m = 1) the attention
 // partials to combine (sa per head of attn_hd elements).
 static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, const _Float16 *nw, float eps,
-                         void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0) {
+                         void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0, bool xf = false) {
     const int64_t N = w.n_out, K = w.k_in;
+    // f32 activations: m <= 2 and the plain row only; 32-bit offsets into X
+    if (xf && (m > 2 || nw || sa || (int64_t)m * K * 4 > 0x7fffffffll)) return RQ_ERR_UNSUPPORTED;
     if (m < 1 || m > 4 || K % 16 != 0 || K > 16 * 256 * 4 || N > 0x7fffffff || !aligned(w.codes, 16) ||
         !aligned(x, 16) || (w.format == RQ_Q_AFFINE_U8 && (w.group % 16 != 0 || K % w.group != 0)))
         return RQ_ERR_UNSUPPORTED;
@@ -529,8 +595,8 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
                attn_hd % 8 != 0 || K % attn_hd != 0))
         return RQ_ERR_UNSUPPORTED;
     int rows;
-    const Decode d = plan(w, w2 != nullptr, nw != nullptr, m, sa, &rows);
-    const bool fx = nw || sa;  // x is an f32 source read by the prologue
+    const Decode d = plan(w, w2 != nullptr, nw != nullptr, m, sa, xf, &rows);
+    const bool fx = nw || sa || xf;  // x is an f32 source
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
                        w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, w2 ? w2->biases : nullptr,
@@ -540,8 +606,8 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     return RQ_OK;
 }
 
-int launch_gemv_decode(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
-    return launch_decode(w, nullptr, x, nullptr, 0.0f, y, yt == RQ_F16 ? kYF16 : kYF32, m, s);
+int launch_gemv_decode(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m, hipStream_t s) {
+    return launch_decode(w, nullptr, x, nullptr, 0.0f, y, yt == RQ_F16 ? kYF16 : kYF32, m, s, 0, 0, xt == RQ_F32);
 }
 
 int launch_gemv_decode_add(const rq_qweight &w, const void *x, float *y, int m, hipStream_t s) {
@@ -553,8 +619,9 @@ int launch_gemv_decode_norm(const rq_qweight &w, const float *x, const _Float16 
     return launch_decode(w, nullptr, x, nw, eps, y, kYF32, 1, s);
 }
 
-int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s) {
-    return launch_decode(gate, &up, x, nullptr, 0.0f, h, kYF16, m, s);
+int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,
+                         hipStream_t s) {
+    return launch_decode(gate, &up, x, nullptr, 0.0f, h, kYF16, m, s, 0, 0, xt == RQ_F32);
 }
 
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,

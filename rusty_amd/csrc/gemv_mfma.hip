@@ -90,11 +90,24 @@ __device__ __forceinline__ half8 u8x8_affine(uint32_t lo, uint32_t hi, float s, 
 // One batch of a wave's operands: 256 k of the block's 16 weight rows, as
 // loaded (4 rows x 256 B per instruction), and the activations of the 8 MFMAs
 // that consume them (16 B per lane per MFMA, already in operand layout).
-template <int FMT>
+template <int FMT, bool XF>
 struct Batch {
-    uint4 w[4], x[8];
+    uint4 w[4], x[XF ? 16 : 8];  // XF: 8 f32 activations (two loads) per MFMA
     float4 s[1], b[1];  // affine only: the four group scales / biases of MFMA row fr
 };
+
+// 8 f32 values x -> hi = fp16(x), lo = fp16(x - hi) (round to nearest even):
+// hi + lo equals x to about 2^-22 relative.
+__device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 &hi, half8 &lo) {
+    const float f[8] = {__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, a.y), __builtin_bit_cast(float, a.z),
+                        __builtin_bit_cast(float, a.w), __builtin_bit_cast(float, b.x), __builtin_bit_cast(float, b.y),
+                        __builtin_bit_cast(float, b.z), __builtin_bit_cast(float, b.w)};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        hi[e] = (_Float16)f[e];
+        lo[e] = (_Float16)(f[e] - (float)hi[e]);
+    }
+}
 
 // SWI: SwiGLU gate/up pass -- the block's 16 weight rows are 8 gate rows (W)
 // and the same 8 rows of the up weight (W2); it writes h = silu(g) * u (fp16).
@@ -103,10 +116,12 @@ struct Batch {
 // biases of its MFMA row for a batch (16 contiguous bytes each, beside the
 // weight loads) and expands the codes to fp16 u*s + b before the MFMA; the
 // epilogue then applies no row scale.
-template <bool SWI, int NWV, int FMT = 0>
+// XF (per-row codes): f32 activations (the reference's dtype), 32 bytes per
+// lane per MFMA, each split into two fp16 terms multiplied separately.
+template <bool SWI, int NWV, int FMT = 0, bool XF = false>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                   const int8_t *__restrict__ W2, const float *__restrict__ scales2,
-                                                  const _Float16 *__restrict__ X, void *__restrict__ Yv, int y_f16,
+                                                  const void *__restrict__ X, void *__restrict__ Yv, int y_f16,
                                                   int m_act, int N, int K, const float *__restrict__ biases,
                                                   const float *__restrict__ biases2) {
     constexpr int RB = SWI ? 8 : 16;  // output rows per block
@@ -122,17 +137,17 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     const int rows_here = min(RB, N - n0);
     const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
-    const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * 2u);
+    const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * (XF ? 4u : 2u));
     // Weight loads: instruction i covers rows 4 i + q, 256 contiguous bytes
     // each (lane chunk fr); SwiGLU: instructions 0-1 the gate rows 0-7, 2-3
     // the up rows 0-7.  A row past the weight, or k past K (which would fall
     // into the next row), reads as zero.
-    const uint32_t xbase = ((uint32_t)fr * (uint32_t)K + 8u * (uint32_t)q) * 2u;
+    const uint32_t xbase = ((uint32_t)fr * (uint32_t)K + 8u * (uint32_t)q) * (XF ? 4u : 2u);
     uint8_t *wl = wt[wave];
     const int nb = (K + 255) / 256;  // 256-k batches; wave w takes batches w, w + NWV, ...
 
     const int Gpr = K / 64;  // affine groups per row
-    auto load = [&](Batch<FMT> &b, int bi) {
+    auto load = [&](Batch<FMT, XF> &b, int bi) {
         const uint32_t k0 = (uint32_t)bi * 256u;
         const bool klive = k0 + 16u * (uint32_t)fr < (uint32_t)K;  // K % 16 == 0
         if constexpr (FMT == 1) {
@@ -156,7 +171,13 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t k = k0 + 32u * (uint32_t)j;  // lane k = k + 8 q .. + 8
-            b.x[j] = bload<0>(rx, k + 8u * (uint32_t)q < (uint32_t)K ? xbase + k * 2u : kOOB);
+            const bool live = k + 8u * (uint32_t)q < (uint32_t)K;
+            if constexpr (XF) {
+                b.x[2 * j] = bload<0>(rx, live ? xbase + k * 4u : kOOB);
+                b.x[2 * j + 1] = bload<0>(rx, live ? xbase + k * 4u + 16u : kOOB);
+            } else {
+                b.x[j] = bload<0>(rx, live ? xbase + k * 2u : kOOB);
+            }
         }
     };
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -164,7 +185,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     // 8 codes of row fr at k = 32 j + 8 q, the k order of its activations.
     // Only this wave touches the slice, and LDS operations of a wave complete
     // in order, so no barrier is needed around it.
-    auto mma = [&](const Batch<FMT> &b) {
+    auto mma = [&](const Batch<FMT, XF> &b) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 4 * i + q;
@@ -189,7 +210,16 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             half8 av;
             if constexpr (FMT == 1) av = u8x8_affine(a[j].x, a[j].y, sg[j / 2], cg[j / 2]);
             else av = i8x8_to_half8(a[j].x, a[j].y);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
+            if constexpr (XF) {
+                // x = hi + lo: the weight operand holds exact code values, so
+                // the two products together keep f32 accuracy
+                half8 hi, lo;
+                f32x8_split(b.x[2 * j], b.x[2 * j + 1], hi, lo);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, hi, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, lo, acc, 0, 0, 0);
+            } else {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
+            }
         }
     };
 
@@ -200,7 +230,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     // the branch, and the prefetch is lost).  mb, the wave's batch count, is
     // wave-uniform.
     const int mb = (nb - wave + NWV - 1) / NWV;
-    Batch<FMT> A, B;
+    Batch<FMT, XF> A, B;
     if (mb > 0) {
         load(A, wave);
         int b = 0;
@@ -268,45 +298,52 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
 
 }  // namespace
 
-static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x, void *y, rq_dtype yt, int m,
-                       hipStream_t s) {
+static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x, rq_dtype xt, void *y, rq_dtype yt,
+                       int m, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
-    const bool affine = w.format == RQ_Q_AFFINE_U8;
-    // 32-bit buffer offsets: 16 activation rows of K fp16 must stay below 2^31 bytes.
-    if (m < 1 || m > 16 || K % 16 != 0 || K > (1 << 24) || N > 0x7fffffff || !aligned(w.codes, 16) || !aligned(x, 16))
+    const bool affine = w.format == RQ_Q_AFFINE_U8, xf = xt == RQ_F32;
+    // 32-bit buffer offsets: 16 activation rows of K values must stay below 2^31 bytes.
+    if (m < 1 || m > 16 || K % 16 != 0 || K > (1 << 24) / (xf ? 2 : 1) || N > 0x7fffffff || !aligned(w.codes, 16) ||
+        !aligned(x, 16))
         return RQ_ERR_UNSUPPORTED;
     if (affine && (w.group != 64 || K % 256 != 0 || (int64_t)N * (K / 64) * 4 > 0xffffffffll)) return RQ_ERR_UNSUPPORTED;
+    // affine codes are expanded to fp16 u*s + b here (one rounding per weight),
+    // which f32 activations would not survive at f32 accuracy
+    if (affine && xf) return RQ_ERR_UNSUPPORTED;
     if (w2 && (w2->format != w.format || !aligned(w2->codes, 16) || (affine && w2->group != w.group)))
         return RQ_ERR_UNSUPPORTED;
     const int64_t blocks = cdiv(N, w2 ? 8 : 16);
-    auto go = [&](auto nwv, auto fmt) {
+    auto go = [&](auto nwv, auto fmt, auto xfc) {
         constexpr int NW = decltype(nwv)::value, F = decltype(fmt)::value;
+        constexpr bool XF = decltype(xfc)::value;
         if (w2)
-            hipLaunchKernelGGL((k_gemv_mfma<true, NW, F>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
-                               (const int8_t *)w.codes, w.scales, (const int8_t *)w2->codes, w2->scales,
-                               (const _Float16 *)x, y, 1, m, (int)N, (int)K, w.biases, w2->biases);
+            hipLaunchKernelGGL((k_gemv_mfma<true, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+                               (const int8_t *)w.codes, w.scales, (const int8_t *)w2->codes, w2->scales, x, y, 1, m,
+                               (int)N, (int)K, w.biases, w2->biases);
         else
-            hipLaunchKernelGGL((k_gemv_mfma<false, NW, F>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
-                               (const int8_t *)w.codes, w.scales, nullptr, nullptr, (const _Float16 *)x, y,
-                               yt == RQ_F16 ? 1 : 0, m, (int)N, (int)K, w.biases, nullptr);
+            hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+                               (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
+                               (int)N, (int)K, w.biases, nullptr);
     };
-    using I8 = std::integral_constant<int, 8>;
-    using I4 = std::integral_constant<int, 4>;
-    using F0 = std::integral_constant<int, 0>;
-    using F1 = std::integral_constant<int, 1>;
+    auto go_x = [&](auto nwv) {
+        if (xf) go(nwv, std::integral_constant<int, 0>{}, std::true_type{});
+        else if (affine) go(nwv, std::integral_constant<int, 1>{}, std::false_type{});
+        else go(nwv, std::integral_constant<int, 0>{}, std::false_type{});
+    };
     const bool wide = K <= 4096 && blocks <= 512;
-    if (affine) wide ? go(I8{}, F1{}) : go(I4{}, F1{});
-    else wide ? go(I8{}, F0{}) : go(I4{}, F0{});
+    if (wide) go_x(std::integral_constant<int, 8>{});
+    else go_x(std::integral_constant<int, 4>{});
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
 
-int launch_gemv_mfma(const rq_qweight &w, const void *x, void *y, rq_dtype yt, int m, hipStream_t s) {
-    return launch_mfma(w, nullptr, x, y, yt, m, s);
+int launch_gemv_mfma(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m, hipStream_t s) {
+    return launch_mfma(w, nullptr, x, xt, y, yt, m, s);
 }
 
-int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, void *h, int m, hipStream_t s) {
-    return launch_mfma(gate, &up, x, h, RQ_F16, m, s);
+int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,
+                       hipStream_t s) {
+    return launch_mfma(gate, &up, x, xt, h, RQ_F16, m, s);
 }
 
 }  // namespace rq

@@ -149,6 +149,34 @@ def test_gemv_f32_output_and_activations(ctx, engine, ydt):
     assert ok
 
 
+# f32 activations, as the reference's Linear passes them, on the decode kernels
+# (m <= 2: the dot2 GEMV; 3-16: the MFMA GEMV): each value is split into two
+# fp16 terms (hi + lo equals it to ~2^-22) and the weights enter as exact code
+# values, so the result keeps f32 accuracy: the f32 bar (1e-5 of max|y|).
+@pytest.mark.parametrize("m,n,k,fmt", [(1, 4096, 4096, 0), (2, 4096, 4096, 0), (3, 1000, 2048, 0),
+                                       (4, 4096, 4096, 0), (8, 1024, 1024, 0), (16, 4096, 4096, 0),
+                                       (5, 333, 4096, 0), (1, 11008, 4096, 0), (1, 4096, 11008, 0),
+                                       (1, 4096, 4096, 1), (2, 1000, 2048, 1)])
+def test_f32_activations_decode_kernels(ctx, engine, m, n, k, fmt):
+    g = synth.rng(900 + m + n + fmt)
+    x = synth.activations(g, m, k, dtype=np.float32)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n, k)
+        b, W = None, QuantizedTensor.rowwise(ctx, q, s)
+    else:
+        q, s, b = synth.affine_weight(g, n, k)
+        W = QuantizedTensor.affine(ctx, q, s, b)
+    truth = orc.qlinear_truth(q, s, b, x, fmt)
+    y = qmm(ctx, engine, W, x, np.float32)
+    max_abs, rel, ok = f32_norm_check(y, truth)
+    report(f"f32 x m={m} {n}x{k} fmt={fmt} -> f32", max_abs, rel)
+    assert ok
+    y16 = qmm(ctx, engine, W, x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y16, truth)
+    report(f"f32 x m={m} {n}x{k} fmt={fmt} -> f16", max_abs, rel)
+    assert ok
+
+
 def test_swiglu_shapes_m8(ctx, engine):
     g = synth.rng(3)
     for n, k in ((11008, 4096), (4096, 11008)):

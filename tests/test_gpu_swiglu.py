@@ -97,6 +97,22 @@ def test_swiglu_generic_paths(ctx, engine):
     assert ok
 
 
+@pytest.mark.parametrize("m", [1, 2, 8])
+def test_swiglu_f32_activations(ctx, engine, m):
+    """f32 activations (the reference's dtype) through the fused gate/up passes
+    (the decode kernel for 1-2 tokens, the matrix-core pass for 3-16): each value
+    split into two fp16 terms, so g and u keep f32 accuracy before h is rounded."""
+    g = synth.rng(700 + m)
+    wg, sg, wu, su, wd, sd = weights(g, 1408, 2048)
+    x = synth.activations(g, m, 2048, dtype=np.float32)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
+    assert ok_h, "intermediate h"
+    max_abs, rel, ok = f16_tol_check(y, orc.swiglu_truth(wg, sg, wu, su, wd, sd, x))
+    print(f"[swiglu f32 x m={m}] max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
 def test_swiglu_shape_error(ctx, engine):
     from rusty_amd import RqError
 
