@@ -93,8 +93,21 @@ __device__ __forceinline__ half8 u8x8_affine(uint32_t lo, uint32_t hi, float s, 
 template <int FMT, bool XF>
 struct Batch {
     uint4 w[4], x[XF ? 16 : 8];  // XF: 8 f32 activations (two loads) per MFMA
-    float4 s[1], b[1];  // affine only: the four group scales / biases of MFMA row fr
+    // affine: the four group scales / biases of MFMA row fr (fp16 expansion);
+    // affine with XF: those of output rows 4 q + r, r < 4 (applied after the MFMAs)
+    float4 s[FMT == 1 && XF ? 4 : 1], b[FMT == 1 && XF ? 4 : 1];
 };
+
+// 8 unsigned affine codes -> their exact fp16 values u (0..255).
+__device__ __forceinline__ half8 u8x8_exact(uint32_t lo, uint32_t hi) {
+    const h2_t k = {(_Float16)1024.0f, (_Float16)1024.0f};
+    uint4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) - k);
+    r.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) - k);
+    r.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) - k);
+    r.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) - k);
+    return __builtin_bit_cast(half8, r);
+}
 
 // 8 f32 values x -> hi = fp16(x), lo = fp16(x - hi) (round to nearest even):
 // hi + lo equals x to about 2^-22 relative.
@@ -116,8 +129,10 @@ __device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 
 // biases of its MFMA row for a batch (16 contiguous bytes each, beside the
 // weight loads) and expands the codes to fp16 u*s + b before the MFMA; the
 // epilogue then applies no row scale.
-// XF (per-row codes): f32 activations (the reference's dtype), 32 bytes per
-// lane per MFMA, each split into two fp16 terms multiplied separately.
+// XF: f32 activations (the reference's dtype), 32 bytes per lane per MFMA,
+// each split into two fp16 terms multiplied separately; per-row codes enter
+// as exact fp16 values, affine codes as exact u with the group's scale and
+// bias applied in f32 after the MFMAs (u . x and the group sum of x).
 template <bool SWI, int NWV, int FMT = 0, bool XF = false>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                   const int8_t *__restrict__ W2, const float *__restrict__ scales2,
@@ -150,7 +165,22 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     auto load = [&](Batch<FMT, XF> &b, int bi) {
         const uint32_t k0 = (uint32_t)bi * 256u;
         const bool klive = k0 + 16u * (uint32_t)fr < (uint32_t)K;  // K % 16 == 0
-        if constexpr (FMT == 1) {
+        if constexpr (FMT == 1 && XF) {
+            // output rows 4 q + r (SwiGLU: rows 0-7 gate, 8-15 up), four groups each
+            const uint32_t bytes = (uint32_t)N * (uint32_t)Gpr * 4u;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int R = 4 * q + rr;
+                const int r = SWI ? R % 8 : R;
+                const bool up = SWI && R >= 8;
+                const uint32_t off = r < rows_here && k0 < (uint32_t)K
+                                         ? ((uint32_t)(n0 + r) * (uint32_t)Gpr + k0 / 64u) * 4u : kOOB;
+                b.s[rr] = __builtin_bit_cast(float4, bload<0>(make_rsrc(up ? scales2 : scales, bytes), off));
+                const float *bp = up ? biases2 : biases;
+                b.b[rr] = bp ? __builtin_bit_cast(float4, bload<0>(make_rsrc(bp, bytes), off))
+                             : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        } else if constexpr (FMT == 1) {
             // MFMA row fr: weight row fr (SwiGLU: gate rows 0-7, up rows 8-15 of the same output rows)
             const int r = SWI ? fr % 8 : fr;
             const bool up = SWI && fr >= 8;
@@ -196,6 +226,37 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         for (int j = 0; j < 8; ++j) {
             const int c = 2 * j + (q >> 1);
             a[j] = *reinterpret_cast<const uint2 *>(wl + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
+        }
+        if constexpr (FMT == 1 && XF) {
+            // exact: per group g (MFMAs 2 g, 2 g + 1), t = u . x and xs = sum x
+            // over the group (ones as the weight operand), then
+            // acc += s . t + b . xs in f32 for output rows 4 q + r
+            half8 ones;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                floatx4 tg = {0.0f, 0.0f, 0.0f, 0.0f}, xg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int j = 2 * gi + jj;
+                    const half8 ue = u8x8_exact(a[j].x, a[j].y);
+                    half8 hi, lo;
+                    f32x8_split(b.x[2 * j], b.x[2 * j + 1], hi, lo);
+                    tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, hi, tg, 0, 0, 0);
+                    tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, lo, tg, 0, 0, 0);
+                    xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, hi, xg, 0, 0, 0);
+                    xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, lo, xg, 0, 0, 0);
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const float sv = gi == 0 ? b.s[rr].x : gi == 1 ? b.s[rr].y : gi == 2 ? b.s[rr].z : b.s[rr].w;
+                    const float bv = gi == 0 ? b.b[rr].x : gi == 1 ? b.b[rr].y : gi == 2 ? b.b[rr].z : b.b[rr].w;
+                    acc[rr] = __builtin_fmaf(sv, tg[rr], acc[rr]);
+                    acc[rr] = __builtin_fmaf(bv, xg[rr], acc[rr]);
+                }
+            }
+            return;
         }
         float sg[4], cg[4];  // affine: MFMA j covers k 32 j .. 32 j + 31, group j / 2 of the batch
         if constexpr (FMT == 1) {
@@ -307,9 +368,6 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
         !aligned(x, 16))
         return RQ_ERR_UNSUPPORTED;
     if (affine && (w.group != 64 || K % 256 != 0 || (int64_t)N * (K / 64) * 4 > 0xffffffffll)) return RQ_ERR_UNSUPPORTED;
-    // affine codes are expanded to fp16 u*s + b here (one rounding per weight),
-    // which f32 activations would not survive at f32 accuracy
-    if (affine && xf) return RQ_ERR_UNSUPPORTED;
     if (w2 && (w2->format != w.format || !aligned(w2->codes, 16) || (affine && w2->group != w.group)))
         return RQ_ERR_UNSUPPORTED;
     const int64_t blocks = cdiv(N, w2 ? 8 : 16);
@@ -325,12 +383,17 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
                                (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
                                (int)N, (int)K, w.biases, nullptr);
     };
-    auto go_x = [&](auto nwv) {
-        if (xf) go(nwv, std::integral_constant<int, 0>{}, std::true_type{});
-        else if (affine) go(nwv, std::integral_constant<int, 1>{}, std::false_type{});
-        else go(nwv, std::integral_constant<int, 0>{}, std::false_type{});
+    auto go_fmt = [&](auto nwv, auto xfc) {
+        if (affine) go(nwv, std::integral_constant<int, 1>{}, xfc);
+        else go(nwv, std::integral_constant<int, 0>{}, xfc);
     };
-    const bool wide = K <= 4096 && blocks <= 512;
+    auto go_x = [&](auto nwv) {
+        if (xf) go_fmt(nwv, std::true_type{});
+        else go_fmt(nwv, std::false_type{});
+    };
+    // affine codes with f32 activations hold four scale and bias vectors per
+    // batch: at 8 waves (256 VGPRs each) they spill, at 4 they fit
+    const bool wide = K <= 4096 && blocks <= 512 && !(affine && xf);
     if (wide) go_x(std::integral_constant<int, 8>{});
     else go_x(std::integral_constant<int, 4>{});
     RQ_LAUNCH_CHECK();

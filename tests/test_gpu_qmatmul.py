@@ -152,11 +152,14 @@ def test_gemv_f32_output_and_activations(ctx, engine, ydt):
 # f32 activations, as the reference's Linear passes them, on the decode kernels
 # (m <= 2: the dot2 GEMV; 3-16: the MFMA GEMV): each value is split into two
 # fp16 terms (hi + lo equals it to ~2^-22) and the weights enter as exact code
-# values, so the result keeps f32 accuracy: the f32 bar (1e-5 of max|y|).
+# values (affine: u, with the group's scale and bias applied in f32), so the
+# result keeps f32 accuracy: the f32 bar (1e-5 of max|y|).
 @pytest.mark.parametrize("m,n,k,fmt", [(1, 4096, 4096, 0), (2, 4096, 4096, 0), (3, 1000, 2048, 0),
                                        (4, 4096, 4096, 0), (8, 1024, 1024, 0), (16, 4096, 4096, 0),
                                        (5, 333, 4096, 0), (1, 11008, 4096, 0), (1, 4096, 11008, 0),
-                                       (1, 4096, 4096, 1), (2, 1000, 2048, 1)])
+                                       (1, 4096, 4096, 1), (2, 1000, 2048, 1), (3, 1000, 2048, 1),
+                                       (4, 4096, 4096, 1), (8, 1024, 1024, 1), (16, 4096, 4096, 1),
+                                       (11, 333, 4096, 1)])
 def test_f32_activations_decode_kernels(ctx, engine, m, n, k, fmt):
     g = synth.rng(900 + m + n + fmt)
     x = synth.activations(g, m, k, dtype=np.float32)

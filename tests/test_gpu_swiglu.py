@@ -126,20 +126,22 @@ def test_swiglu_shape_error(ctx, engine):
         engine.mlp_swiglu(ctx, X, G, U, Dbad, Y)
 
 
-@pytest.mark.parametrize("m,hidden", [(1, 1024), (2, 1024), (1, 4096), (2, 2560), (8, 1024), (16, 1024)])
-def test_swiglu_affine_weights(ctx, engine, m, hidden):
+@pytest.mark.parametrize("m,hidden,xdt", [(1, 1024, np.float16), (2, 1024, np.float16), (1, 4096, np.float16),
+                                         (2, 2560, np.float16), (8, 1024, np.float16), (16, 1024, np.float16),
+                                         (1, 2048, np.float32), (4, 2048, np.float32), (16, 1024, np.float32)])
+def test_swiglu_affine_weights(ctx, engine, m, hidden, xdt):
     """The MLP on the reference's affine weights (u8, scale + bias per 64): gate and
     up in one pass with the silu*mul epilogue -- the decode kernel's SwiGLU pass
     for 1-2 tokens (row groups of 64/256 threads, 1-3 chunks per thread), the
     matrix-core pass for 3-16."""
-    g = synth.rng(500 + m + hidden)
+    g = synth.rng(500 + m + hidden + (xdt == np.float32))
     inter = 320
     ug, sg, bg = synth.affine_weight(g, inter, hidden)
     uu, su, bu = synth.affine_weight(g, inter, hidden)
     ud, sd, bd = synth.affine_weight(g, hidden, inter)
     G, U, D = (QuantizedTensor.affine(ctx, *a) for a in ((ug, sg, bg), (uu, su, bu), (ud, sd, bd)))
-    x = synth.activations(g, m, hidden)
-    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+    x = synth.activations(g, m, hidden, dtype=xdt)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16 if xdt == np.float16 else DType.FP32)
     Y = UnifiedTensor.new(ctx, np.full((m, hidden), np.nan, np.float32), dtype=DType.FP32)
     h = engine.mlp_swiglu(ctx, X, G, U, D, Y)
     gt = orc.qlinear_truth(ug, sg, bg, x.astype(np.float32), 1)
