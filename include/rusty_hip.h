@@ -176,7 +176,10 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * forward (Linear::forward, rusty-graph/src/lib.rs:69-70 ->
  * Tensor::matmul, rusty-autograd/src/lib.rs:468-477).
  * x_dtype/y_dtype: RQ_F16 or RQ_F32; accumulation is f32.
- * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM.  On the
+ * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM.  f32
+ * activations keep f32 accuracy up to m = 16 (each value carried as two fp16
+ * terms, the weights as exact code values); the GEMM rounds them to fp16
+ * (the fp16-MFMA prefill path), as it does affine weights.  On the
  * context's own stream (stream NULL) a GEMM with few tokens splits K over
  * more blocks using the context's workspace, so two such calls of one
  * context must not run concurrently (they cannot on one stream); on any
