@@ -178,7 +178,9 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * x_dtype/y_dtype: RQ_F16 or RQ_F32; accumulation is f32.
  * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM.  f32
  * activations keep f32 accuracy up to m = 16 (each value carried as two fp16
- * terms, the weights as exact code values); the GEMM rounds them to fp16
+ * terms, the weights as exact code values) for values in fp16's range
+ * (|x| <= 65504; below 6.1e-5 a value keeps fp16-subnormal precision, which
+ * matters only if a whole row is that small); the GEMM rounds them to fp16
  * (the fp16-MFMA prefill path), as it does affine weights.  On the
  * context's own stream (stream NULL) a GEMM with few tokens splits K over
  * more blocks using the context's workspace, so two such calls of one
