@@ -488,11 +488,15 @@ int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, co
     if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4)
         st = launch_swiglu_decode(gate, up, x, x_dtype, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && m > 16) {
-        // prefill: gate and up through the GEMM into the two halves of the
-        // workspace, then h = silu(g) * u in place over the first half
+        // prefill: gate and up through the GEMM (one launch for the pair where
+        // it serves them) into the two halves of the workspace, then
+        // h = silu(g) * u in place over the first half
         _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
-        st = launch_gemm(gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, ws, s);
-        if (st == RQ_OK) st = launch_gemm(up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, ws, s);
+        st = launch_gemm_pair(gate, up, x, x_dtype, g, u, RQ_F16, m, ctx->num_cus, ws, s);
+        if (st == RQ_ERR_UNSUPPORTED) {
+            st = launch_gemm(gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, ws, s);
+            if (st == RQ_OK) st = launch_gemm(up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, ws, s);
+        }
         if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
     }
     if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(gate, up, x, x_dtype, h, m, s);

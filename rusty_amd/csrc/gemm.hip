@@ -84,6 +84,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
 }
 
+// A resource whose base and size are wave-uniform values the compiler might
+// still hold in VGPRs (the DMA's inline asm takes its resource in SGPRs):
+// both are passed through readfirstlane first.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_s(const void *p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return make_rsrc(reinterpret_cast<const void *>((hi << 32) | lo),
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
+}
+
 // DMA of 16 bytes per lane: LDS[lds_addr + 16 * lane] = buffer[voff], with
 // lds_addr a 32-bit LDS address (uniform across the wave).  Issued
 // as inline asm so the compiler does not turn its conservative LDS-DMA alias
@@ -177,12 +188,20 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
 // k-step's values for the block's BN features are contiguous: each wave
 // stages 64 of them per k-step (one 4-byte DMA per lane) beside its X stage,
 // and the weight is expanded to fp16 u*s + b while the fragments are read.
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, int FMT = 0>
+// PAIR, a weight pair (per-row codes): rows [0, n_split) of the product come
+// from (W, scales) into Yv ([M][n_split]), rows [n_split, N) from (Wb,
+// scalesb) into Yb ([M][N - n_split]); n_split is a multiple of BN, so a tile
+// reads one weight and writes one output.  Only the two large tiles are built
+// with it (the smaller ones run near the SGPR limit already).
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, int FMT = 0,
+          bool PAIR = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm, int splits, float *__restrict__ skw,
-                                                     int *__restrict__ skc, int group) {
+                                                     int *__restrict__ skc, int group, const uint8_t *__restrict__ Wb,
+                                                     const float *__restrict__ scalesb, void *__restrict__ Yb,
+                                                     int n_split) {
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -226,8 +245,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     const int nk_all = K / 64, ks = (nk_all + splits - 1) / splits;
     const int k0 = split * ks, nk = min(ks, nk_all - k0);  // this block's k-steps [k0, k0 + nk)
 
-    const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
-    const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
+    // the pair member this tile belongs to: its weight rows, scales and output
+    const bool second = PAIR && n0 >= n_split;
+    const int nw0 = second ? n0 - n_split : n0;            // first row within that weight
+    const int NL = PAIR ? (second ? N - n_split : n_split) : N;  // its rows (and its output's row length)
+    const float *__restrict__ scl = second ? scalesb : scales;
+    void *__restrict__ Yo = second ? Yb : Yv;
+    // (PAIR: the compiler keeps some of these uniform values in VGPRs)
+    const auto rx = PAIR ? make_rsrc_s(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u)
+                         : make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
+    const auto rw = PAIR ? make_rsrc_s((second ? Wb : W) + (size_t)nw0 * K, (uint32_t)min(BN, NL - nw0) * (uint32_t)K)
+                         : make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
     // affine: lane l of wave w stages value i = 64 w + l of [s | c] for the
     // block's features (rows past N and lanes past 2 BN read zero); the
     // transposed scales hold 2 N floats per group
@@ -619,7 +647,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     // lanes, with the non-temporal policy.  Writing straight from the MFMA
     // layout puts 8-byte pieces of 32 rows in every store instruction; staged,
     // 2048x4096x4096 took 70.9 -> 67.6 us, N = 11008 194.6 -> 182.5 us.
-    if ((y_f16 ? N % 8 == 0 : N % 4 == 0) && (int64_t)BM * N * (y_f16 ? 2 : 4) < (1ll << 31)) {
+    if ((y_f16 ? NL % 8 == 0 : NL % 4 == 0) && (int64_t)BM * NL * (y_f16 ? 2 : 4) < (1ll << 31)) {
         auto staged = [&](auto eb_c) {
             constexpr int EB = decltype(eb_c)::value;  // output element bytes
             constexpr int RS = BN * EB + 16;           // padded LDS row stride
@@ -634,7 +662,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     const int fl = wn * TN + i * 32 + 8 * g + h * 4;  // feature within the tile
                     float sc[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sc[r] = n0 + fl + r < N ? (FMT == 0 ? scales[n0 + fl + r] : 1.0f) : 0.0f;
+                    for (int r = 0; r < 4; ++r) sc[r] = nw0 + fl + r < NL ? (FMT == 0 ? scl[nw0 + fl + r] : 1.0f) : 0.0f;
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
                         uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
@@ -655,15 +683,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
             constexpr int RPP = 64 * NW / CPR;  // rows per pass
             static_assert(BM % RPP == 0, "copy-out passes");
             // rows past M fall outside the resource; pieces past N are masked
-            const auto ry = make_rsrc(static_cast<uint8_t *>(Yv) + ((size_t)m0 * N + n0) * EB,
-                                      (uint32_t)min(BM, M - m0) * (uint32_t)N * EB);
+            const auto ry = make_rsrc(static_cast<uint8_t *>(Yo) + ((size_t)m0 * NL + nw0) * EB,
+                                      (uint32_t)min(BM, M - m0) * (uint32_t)NL * EB);
             const int c = t % CPR;
-            const bool col_ok = n0 + c * (16 / EB) < N;
+            const bool col_ok = nw0 + c * (16 / EB) < NL;
 #pragma unroll
             for (int ps = 0; ps < BM / RPP; ++ps) {
                 const int row = ps * RPP + t / CPR;
                 const uint4 v = *reinterpret_cast<const uint4 *>(ot + row * RS + c * 16);
-                const uint32_t off = col_ok ? (uint32_t)row * (uint32_t)N * EB + (uint32_t)c * 16u : kOOB;
+                const uint32_t off = col_ok ? (uint32_t)row * (uint32_t)NL * EB + (uint32_t)c * 16u : kOOB;
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ry, off, 0, 2);
             }
         };
@@ -676,10 +704,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;
+            const int nb = nw0 + wn * TN + i * 32 + 8 * g + h * 4;  // row within this tile's weight
             float sc[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? (FMT == 0 ? scales[nb + r] : 1.0f) : 0.0f;
+            for (int r = 0; r < 4; ++r) sc[r] = nb + r < NL ? (FMT == 0 ? scl[nb + r] : 1.0f) : 0.0f;
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int mm = m0 + wm * TM + j * 32 + fr;
@@ -687,22 +715,22 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r];
-                const size_t o = (size_t)mm * N + nb;
-                if (nb + 4 <= N && (N % 4) == 0) {
+                const size_t o = (size_t)mm * NL + nb;
+                if (nb + 4 <= NL && (NL % 4) == 0) {
                     if (y_f16) {
                         const h2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
-                        *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yv) + o) =
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yo) + o) =
                             make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
                     } else {
-                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yv) + o) =
+                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yo) + o) =
                             make_float4(v[0], v[1], v[2], v[3]);
                     }
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        if (nb + r >= N) break;
-                        if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o + r] = (_Float16)v[r];
-                        else reinterpret_cast<float *>(Yv)[o + r] = v[r];
+                        if (nb + r >= NL) break;
+                        if (y_f16) reinterpret_cast<_Float16 *>(Yo)[o + r] = (_Float16)v[r];
+                        else reinterpret_cast<float *>(Yo)[o + r] = v[r];
                     }
                 }
             }
@@ -720,9 +748,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 // N = 11008: 19.0 -> 17.7 (2).  Only on the context's own stream (ws.partials
 // is null otherwise); the larger tiles gained nothing from splitting (their
 // LDS rings allow one block per CU).
-template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false>
+// The second member of a weight pair (see k_gemm_rowwise); n_split 0: none.
+struct GemmPair {
+    const uint8_t *w = nullptr;
+    const float *scales = nullptr;
+    void *y = nullptr;
+    int64_t n_split = 0;
+};
+
+template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, bool PAIR = false>
 int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
-                 int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s) {
+                 int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{}) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
@@ -737,9 +773,11 @@ int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * splits)), dim3(64 * NW), 0, s, (const uint8_t *)w.codes,
                            scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m,
-                           tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64);
+                           tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64,
+                           pair.w, pair.scales, pair.y, (int)(pair.n_split ? pair.n_split : N));
     };
-    if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
+    if constexpr (PAIR) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, true>);
+    else if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
     else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0>);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
@@ -783,7 +821,7 @@ __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, _
 
 // The fp16-activation GEMM over m rows, tile chosen by shape.
 int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
-               int64_t cus, const GemmWorkspace &ws, hipStream_t s) {
+               int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{}) {
     const int64_t N = w.n_out;
     // The largest tile whose grid still has >= 2/3 as many tiles as the device
     // has CUs: a block streams its X and W panels through one CU at a latency-
@@ -803,6 +841,13 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
     // a tile taller than the tokens (rounded up to 64) only multiplies padding:
     // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
     auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
+    if (pair.n_split) {  // a weight pair: the two large tiles only (the caller falls back otherwise)
+        if (fills(128, 256))
+            return launch_tiled<128, 256, true, 4, 8, 4, 2, true, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, pair);
+        if (fills(128, 128))
+            return launch_tiled<128, 128, true, 4, 8, 2, 2, true, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, pair);
+        return RQ_ERR_UNSUPPORTED;
+    }
     if (fills(128, 256)) return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
     if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
     if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
@@ -818,6 +863,31 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
 // preparation area (context stream only): the scales transposed to
 // [group][row] and/or the activations cast to fp16, a chunk of rows at a time
 // when they do not fit, each chunk then multiplied by the same kernel.
+// Two per-row int8 weights of one input size in one launch (SwiGLU's gate and
+// up): Ya = X . deq(a)^T, Yb = X . deq(b)^T.  Their rows form one grid of
+// a.n_out + b.n_out, so the tile heuristic sees the combined width (at 512
+// tokens x 5632 features: 128x256 tiles over both instead of two launches of
+// 128x128 tiles that each leave a third of the CUs idle).  a.n_out must be a
+// multiple of 256 (every tile width), fp16 activations.
+int launch_gemm_pair(const rq_qweight &a, const rq_qweight &b, const void *x, rq_dtype xt, void *ya, void *yb,
+                     rq_dtype yt, int64_t m, int num_cus, const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t K = a.k_in, N = a.n_out + b.n_out;
+    if (a.format != RQ_Q_ROWWISE_I8 || b.format != RQ_Q_ROWWISE_I8 || b.k_in != K || xt != RQ_F16 ||
+        a.n_out % 256 != 0 || K % 64 != 0 || K > (1 << 21) || !aligned(a.codes, 16) || !aligned(b.codes, 16) ||
+        !aligned(x, 16) || m > 0x7fffffff || N > 0x7fffffff)
+        return RQ_ERR_UNSUPPORTED;
+    if (yt == RQ_F16 ? !aligned(ya, 8) || !aligned(yb, 8) : !aligned(ya, 16) || !aligned(yb, 16))
+        return RQ_ERR_UNSUPPORTED;
+    rq_qweight w = a;
+    w.n_out = N;
+    GemmPair pair;
+    pair.w = static_cast<const uint8_t *>(b.codes);
+    pair.scales = b.scales;
+    pair.y = yb;
+    pair.n_split = a.n_out;
+    return gemm_tiles(w, a.scales, 0, x, ya, yt, m, num_cus > 0 ? num_cus : 256, ws, s, pair);
+}
+
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;

