@@ -148,13 +148,14 @@ __global__ __launch_bounds__(NT) void k_rope_scatter(const float *__restrict__ q
 // wave fills was last read two tiles earlier, before the previous barrier);
 // their partial softmaxes (running max m, sum l, unnormalised O) combine
 // through LDS at the end, each wave finishing 16 / NW of every lane's
-// accumulator entries.  p0 is a
-// multiple of 32, so every query tile starts a key tile and every key tile a
-// query reaches holds a key at or before it: the running max of a wave that
-// had a tile is finite, and a wave that had none weighs e^-inf = 0.
-// Measured at 512 positions, 32 heads of 64 (one wave per CU-round of
-// blocks matters more than the chain per wave): NW = 4 11.6 us, 8 16.9 us
-// (155 VGPRs: one 8-wave block per CU, two rounds), 2 14.2 us, 1 22.7 us.
+// accumulator entries.  p0 is a multiple of 32, so every query tile starts a
+// key tile and every key tile a query reaches holds a key at or before it:
+// the running max of a wave that had a tile is finite, and a wave that had
+// none weighs 2^-inf = 0.
+// Measured at 512 positions, 32 heads of 64 (before the 2^x exponentials,
+// which took NW = 4 from 11.6 to 10.8 us): NW = 4 11.6 us, 8 16.9 us (155
+// VGPRs allow one 8-wave block per CU, so the grid needs two dispatch
+// passes), 2 14.2 us, 1 22.7 us.
 template <int HD, int NW>
 __global__ __launch_bounds__(NW * 64) void k_attn_prefill(const _Float16 *__restrict__ q, const _Float16 *__restrict__ kc,
                                                       const _Float16 *__restrict__ vc, _Float16 *__restrict__ out,
