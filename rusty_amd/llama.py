@@ -129,7 +129,8 @@ def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaH
     embedding is tied to the lm_head (:242-249).  The runner's embedding table
     is fp16: a quantized ``model.embed_tokens`` is dequantized on the host
     (u * s + b in f64) and rounded to fp16, norms are rounded to fp16.
-    ``max_seq`` defaults to ``max_position_embeddings`` (else 2048)."""
+    ``max_seq`` defaults to ``max_position_embeddings`` (else 2048), capped at
+    the runner's 32768 positions."""
     from pathlib import Path
 
     from .loader import LoaderError, QuantizationConfig, WeightsContext, load_config
@@ -144,7 +145,7 @@ def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaH
         n_kv_heads=int(conf.get("num_key_value_heads") or heads),
         head_dim=int(conf.get("head_dim") or hidden // heads), intermediate=int(conf["intermediate_size"]),
         vocab=int(conf["vocab_size"]),
-        max_seq=int(max_seq or conf.get("max_position_embeddings") or 2048),
+        max_seq=int(max_seq or min(int(conf.get("max_position_embeddings") or 2048), 32768)),
         norm_eps=float(conf.get("norm_eps", conf.get("rms_norm_eps", 1e-5))),
         rope_theta=float(conf.get("rope_theta", 10000.0)))
     wc = WeightsContext()

@@ -74,6 +74,19 @@ def test_mlx_names_untied_plain_embed(tmp_path):
                                   _codes(t["model.layers.1.mlp.down_proj.weight"][1], CFG.hidden))
 
 
+def test_max_seq_default_capped(tmp_path):
+    import json
+
+    write_mlx_llama(tmp_path, CFG, seed=5, files=1)
+    conf = json.loads((tmp_path / "config.json").read_text())
+    conf["max_position_embeddings"] = 131072
+    (tmp_path / "config.json").write_text(json.dumps(conf))
+    cfg, _ = load_mlx(tmp_path)
+    assert cfg.max_seq == 32768
+    cfg, _ = load_mlx(tmp_path, max_seq=1000)
+    assert cfg.max_seq == 1000
+
+
 def test_loader_errors(tmp_path):
     t = write_mlx_llama(tmp_path, CFG, seed=3, files=1)
     # a Linear stored unquantized: the runner takes quantized Linears only
