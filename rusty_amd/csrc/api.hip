@@ -476,7 +476,7 @@ int rq::swiglu_check(const rq_qweight *gate, const rq_qweight *up, const rq_qwei
 
 // The SwiGLU MLP over validated arguments, h a workspace of 2*m*I fp16 values:
 // the gate/up pass writes h = silu(g) * u into its first m*I values (the
-// prefill path stages g and u in its two halves first), then the down
+// prefill fallback stages g and u in its two halves first), then the down
 // projection reads it.  ws: the split-K workspace the prefill GEMMs may use.
 int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, const rq_qweight &down, const void *x,
                    rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, const GemmWorkspace &ws,
@@ -488,16 +488,16 @@ int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, co
     if (st == RQ_ERR_UNSUPPORTED && x_dtype == RQ_F16 && m <= 4)
         st = launch_swiglu_decode(gate, up, x, x_dtype, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && m > 16) {
-        // prefill: gate and up through the GEMM (one launch for the pair where
-        // it serves them) into the two halves of the workspace, then
-        // h = silu(g) * u in place over the first half
-        _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
-        st = launch_gemm_pair(gate, up, x, x_dtype, g, u, RQ_F16, m, ctx->num_cus, ws, s);
+        // prefill: gate and up in one GEMM launch with the silu*mul epilogue
+        // where it serves them; else two GEMMs into the two halves of the
+        // workspace, then h = silu(g) * u in place over the first half
+        st = launch_gemm_swiglu(gate, up, x, x_dtype, h, m, ctx->num_cus, ws, s);
         if (st == RQ_ERR_UNSUPPORTED) {
+            _Float16 *g = static_cast<_Float16 *>(h), *u = g + m * I;
             st = launch_gemm(gate, x, x_dtype, g, RQ_F16, m, ctx->num_cus, ws, s);
             if (st == RQ_OK) st = launch_gemm(up, x, x_dtype, u, RQ_F16, m, ctx->num_cus, ws, s);
+            if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
         }
-        if (st == RQ_OK) st = launch_silu_mul(g, u, g, m * I, s);
     }
     if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(gate, up, x, x_dtype, h, m, s);
     if (st != RQ_OK) return st;

@@ -99,10 +99,11 @@ struct GemmWorkspace {
 GemmWorkspace gemm_workspace(const rq_ctx *ctx, hipStream_t s);
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s);
-// Ya = X . deq(a)^T and Yb = X . deq(b)^T in one GEMM launch (per-row int8,
-// fp16 X, a.n_out % 256 == 0); RQ_ERR_UNSUPPORTED otherwise.
-int launch_gemm_pair(const rq_qweight &a, const rq_qweight &b, const void *x, rq_dtype xt, void *ya, void *yb,
-                     rq_dtype yt, int64_t m, int num_cus, const GemmWorkspace &ws, hipStream_t s);
+// h = fp16(silu(X . deq(gate)^T) * (X . deq(up)^T)) in one GEMM launch, g and
+// u rounded to fp16 before the silu*mul (per-row int8, fp16 X, I % 8 == 0, a
+// grid that fills the device); RQ_ERR_UNSUPPORTED otherwise.
+int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
+                       int num_cus, const GemmWorkspace &ws, hipStream_t s);
 int launch_qlinear_generic(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
                            int64_t m, hipStream_t s);
 int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,

@@ -188,11 +188,13 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
 // k-step's values for the block's BN features are contiguous: each wave
 // stages 64 of them per k-step (one 4-byte DMA per lane) beside its X stage,
 // and the weight is expanded to fp16 u*s + b while the fragments are read.
-// PAIR, a weight pair (per-row codes): rows [0, n_split) of the product come
-// from (W, scales) into Yv ([M][n_split]), rows [n_split, N) from (Wb,
-// scalesb) into Yb ([M][N - n_split]); n_split is a multiple of BN, so a tile
-// reads one weight and writes one output.  Only the two large tiles are built
-// with it (the smaller ones run near the SGPR limit already).
+// PAIR, SwiGLU's gate and up (per-row codes, n_split = I rows each, N = 2 I):
+// tile column block tn covers rows [j0, j0 + BN/2) of both weights, j0 =
+// tn * BN/2 -- the gate (W, scales) in tile columns [0, BN/2), the up weight
+// (Wb, scalesb) in [BN/2, BN) -- and the epilogue writes h = silu(g) * u
+// (g and u rounded to fp16 first, as a separate silu*mul pass over stored
+// g and u would see them) to Yv, fp16 [M][I] (I % 8 == 0).  Only the two
+// large tiles are built with it (the smaller ones run near the SGPR limit).
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, int FMT = 0,
           bool PAIR = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restrict__ W, const float *__restrict__ scales,
@@ -200,8 +202,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm, int splits, float *__restrict__ skw,
                                                      int *__restrict__ skc, int group, const uint8_t *__restrict__ Wb,
-                                                     const float *__restrict__ scalesb, void *__restrict__ Yb,
-                                                     int n_split) {
+                                                     const float *__restrict__ scalesb, int n_split) {
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -245,17 +246,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     const int nk_all = K / 64, ks = (nk_all + splits - 1) / splits;
     const int k0 = split * ks, nk = min(ks, nk_all - k0);  // this block's k-steps [k0, k0 + nk)
 
-    // the pair member this tile belongs to: its weight rows, scales and output
-    const bool second = PAIR && n0 >= n_split;
-    const int nw0 = second ? n0 - n_split : n0;            // first row within that weight
-    const int NL = PAIR ? (second ? N - n_split : n_split) : N;  // its rows (and its output's row length)
-    const float *__restrict__ scl = second ? scalesb : scales;
-    void *__restrict__ Yo = second ? Yb : Yv;
+    // PAIR: the tile's first row in each weight, the rows per weight (and h's row length)
+    constexpr int HB = BN / 2;
+    const int nw0 = PAIR ? n0 / 2 : n0;
+    const int NL = PAIR ? n_split : N;
     // (PAIR: the compiler keeps some of these uniform values in VGPRs)
     const auto rx = PAIR ? make_rsrc_s(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u)
                          : make_rsrc(X + (size_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K * 2u);
-    const auto rw = PAIR ? make_rsrc_s((second ? Wb : W) + (size_t)nw0 * K, (uint32_t)min(BN, NL - nw0) * (uint32_t)K)
+    const auto rw = PAIR ? make_rsrc_s(W + (size_t)nw0 * K, (uint32_t)min(HB, NL - nw0) * (uint32_t)K)
                          : make_rsrc(W + (size_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
+    const auto rwb = PAIR ? make_rsrc_s(Wb + (size_t)nw0 * K, (uint32_t)min(HB, NL - nw0) * (uint32_t)K) : rw;
     // affine: lane l of wave w stages value i = 64 w + l of [s | c] for the
     // block's features (rows past N and lanes past 2 BN read zero); the
     // transposed scales hold 2 N floats per group
@@ -280,8 +280,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         if constexpr (W2) {
             // 8 rows x 128 bytes (two k-steps) per unit, chunk s of row r holding
             // global chunk s ^ ((r >> 1) & 7)
+            // (PAIR: tile rows from HB on are rows of the up weight)
             const int row = (wave * WUW + q) * 8 + lane / 8, s = lane % 8;
-            woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 1) & 7)) * 16;
+            const int wr = PAIR && row >= HB ? row - HB : row;
+            woff[q] = (uint32_t)wr * K + (uint32_t)(s ^ ((row >> 1) & 7)) * 16;
         } else {
             const int row = (wave * WUW + q) * 16 + lane / 4, s = lane % 4;
             woff[q] = (uint32_t)row * K + (uint32_t)(s ^ ((row >> 2) & 3)) * 16;
@@ -314,7 +316,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         kt += k0;
         const uint32_t sw = ring_lds + (uint32_t)(S * BM * 128) + (uint32_t)pair * (uint32_t)(BN * 128);
 #pragma unroll
-        for (int q = 0; q < WUW; ++q) dma16(rw, sw + (uint32_t)(wave * WUW + q) * 1024u, live ? woff[q] + kt * 64 : kOOB);
+        for (int q = 0; q < WUW; ++q)
+            dma16(PAIR && (wave * WUW + q) * 8 >= HB ? rwb : rw, sw + (uint32_t)(wave * WUW + q) * 1024u,
+                  live ? woff[q] + kt * 64 : kOOB);
     };
 
     floatx16 acc[FN][FM];
@@ -647,90 +651,114 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     // lanes, with the non-temporal policy.  Writing straight from the MFMA
     // layout puts 8-byte pieces of 32 rows in every store instruction; staged,
     // 2048x4096x4096 took 70.9 -> 67.6 us, N = 11008 194.6 -> 182.5 us.
-    if ((y_f16 ? NL % 8 == 0 : NL % 4 == 0) && (int64_t)BM * NL * (y_f16 ? 2 : 4) < (1ll << 31)) {
-        auto staged = [&](auto eb_c) {
-            constexpr int EB = decltype(eb_c)::value;  // output element bytes
-            constexpr int RS = BN * EB + 16;           // padded LDS row stride
-            static_assert(BM * RS <= RING, "output staging does not fit in the ring");
-            uint8_t *ot = reinterpret_cast<uint8_t *>(&ring[0]);
-            __syncthreads();  // every wave is done with the ring (and the k-group exchange)
+    // PAIR stages g and u as fp16 and leaves as h = silu(g) * u.
+    auto staged = [&](auto eb_c) {
+        constexpr int EB = decltype(eb_c)::value;  // staged element bytes
+        constexpr int RS = BN * EB + 16;           // padded LDS row stride
+        static_assert(BM * RS <= RING, "output staging does not fit in the ring");
+        uint8_t *ot = reinterpret_cast<uint8_t *>(&ring[0]);
+        __syncthreads();  // every wave is done with the ring (and the k-group exchange)
 #pragma unroll
-            for (int i = 0; i < FN; ++i) {
-                if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
+        for (int i = 0; i < FN; ++i) {
+            if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int fl = wn * TN + i * 32 + 8 * g + h * 4;  // feature within the tile
-                    float sc[4];
+            for (int g = 0; g < 4; ++g) {
+                const int fl = wn * TN + i * 32 + 8 * g + h * 4;  // feature within the tile
+                // its weight row and scales (PAIR: wave-uniform choice of gate or up)
+                const bool upc = PAIR && fl >= HB;
+                const int wr = nw0 + (upc ? fl - HB : fl);
+                const float *__restrict__ scl = upc ? scalesb : scales;
+                float sc[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sc[r] = nw0 + fl + r < NL ? (FMT == 0 ? scl[nw0 + fl + r] : 1.0f) : 0.0f;
+                for (int r = 0; r < 4; ++r) sc[r] = wr + r < NL ? (FMT == 0 ? scl[wr + r] : 1.0f) : 0.0f;
 #pragma unroll
-                    for (int j = 0; j < FM; ++j) {
-                        uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
-                        const float v0 = acc[i][j][4 * g] * sc[0], v1 = acc[i][j][4 * g + 1] * sc[1];
-                        const float v2 = acc[i][j][4 * g + 2] * sc[2], v3 = acc[i][j][4 * g + 3] * sc[3];
-                        if constexpr (EB == 2) {
-                            const h2_t lo = {(_Float16)v0, (_Float16)v1}, hi = {(_Float16)v2, (_Float16)v3};
-                            *reinterpret_cast<uint2 *>(dst) =
-                                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-                        } else {
-                            *reinterpret_cast<float4 *>(dst) = make_float4(v0, v1, v2, v3);
-                        }
+                for (int j = 0; j < FM; ++j) {
+                    uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
+                    const float v0 = acc[i][j][4 * g] * sc[0], v1 = acc[i][j][4 * g + 1] * sc[1];
+                    const float v2 = acc[i][j][4 * g + 2] * sc[2], v3 = acc[i][j][4 * g + 3] * sc[3];
+                    if constexpr (EB == 2) {
+                        const h2_t lo = {(_Float16)v0, (_Float16)v1}, hi = {(_Float16)v2, (_Float16)v3};
+                        *reinterpret_cast<uint2 *>(dst) =
+                            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                    } else {
+                        *reinterpret_cast<float4 *>(dst) = make_float4(v0, v1, v2, v3);
                     }
                 }
             }
-            __syncthreads();
-            constexpr int CPR = BN * EB / 16;   // 16-byte pieces per tile row
-            constexpr int RPP = 64 * NW / CPR;  // rows per pass
-            static_assert(BM % RPP == 0, "copy-out passes");
-            // rows past M fall outside the resource; pieces past N are masked
-            const auto ry = make_rsrc(static_cast<uint8_t *>(Yo) + ((size_t)m0 * NL + nw0) * EB,
-                                      (uint32_t)min(BM, M - m0) * (uint32_t)NL * EB);
-            const int c = t % CPR;
-            const bool col_ok = nw0 + c * (16 / EB) < NL;
+        }
+        __syncthreads();
+        constexpr int OB = PAIR ? HB * 2 : BN * EB;  // output bytes per tile row
+        constexpr int CPR = OB / 16;                 // 16-byte pieces per tile row
+        constexpr int RPP = 64 * NW / CPR;           // rows per pass
+        static_assert(BM % RPP == 0, "copy-out passes");
+        constexpr int OE = PAIR ? 2 : EB;            // output element bytes
+        // rows past M fall outside the resource; pieces past the row are masked
+        const auto ry = make_rsrc(static_cast<uint8_t *>(Yv) + ((size_t)m0 * NL + nw0) * OE,
+                                  (uint32_t)min(BM, M - m0) * (uint32_t)NL * OE);
+        const int c = t % CPR;
+        const bool col_ok = nw0 + c * (16 / OE) < NL;
 #pragma unroll
-            for (int ps = 0; ps < BM / RPP; ++ps) {
-                const int row = ps * RPP + t / CPR;
-                const uint4 v = *reinterpret_cast<const uint4 *>(ot + row * RS + c * 16);
-                const uint32_t off = col_ok ? (uint32_t)row * (uint32_t)NL * EB + (uint32_t)c * 16u : kOOB;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ry, off, 0, 2);
+        for (int ps = 0; ps < BM / RPP; ++ps) {
+            const int row = ps * RPP + t / CPR;
+            uint4 v = *reinterpret_cast<const uint4 *>(ot + row * RS + c * 16);
+            if constexpr (PAIR) {
+                // silu(g) * u in f32 (v / (1 + e^-v), the reference's silu), rounded to fp16
+                const half8 gv = __builtin_bit_cast(half8, v);
+                const half8 uv = *reinterpret_cast<const half8 *>(ot + row * RS + HB * 2 + c * 16);
+                half8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float gf = (float)gv[e];
+                    hv[e] = (_Float16)(gf / (1.0f + expf(-gf)) * (float)uv[e]);
+                }
+                v = __builtin_bit_cast(uint4, hv);
             }
-        };
-        if (y_f16) staged(std::integral_constant<int, 2>{});
-        else staged(std::integral_constant<int, 4>{});
+            const uint32_t off = col_ok ? (uint32_t)row * (uint32_t)NL * OE + (uint32_t)c * 16u : kOOB;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ry, off, 0, 2);
+        }
+    };
+    if constexpr (PAIR) {
+        staged(std::integral_constant<int, 2>{});  // the host guarantees I % 8 == 0 and fp16 h
         return;
-    }
+    } else {
+        if ((y_f16 ? NL % 8 == 0 : NL % 4 == 0) && (int64_t)BM * NL * (y_f16 ? 2 : 4) < (1ll << 31)) {
+            if (y_f16) staged(std::integral_constant<int, 2>{});
+            else staged(std::integral_constant<int, 4>{});
+            return;
+        }
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
-        if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
+        for (int i = 0; i < FN; ++i) {
+            if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int nb = nw0 + wn * TN + i * 32 + 8 * g + h * 4;  // row within this tile's weight
-            float sc[4];
+            for (int g = 0; g < 4; ++g) {
+                const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;  // weight row
+                float sc[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = nb + r < NL ? (FMT == 0 ? scl[nb + r] : 1.0f) : 0.0f;
+                for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? (FMT == 0 ? scales[nb + r] : 1.0f) : 0.0f;
 #pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const int mm = m0 + wm * TM + j * 32 + fr;
-                if (mm >= M) continue;
-                float v[4];
+                for (int j = 0; j < FM; ++j) {
+                    const int mm = m0 + wm * TM + j * 32 + fr;
+                    if (mm >= M) continue;
+                    float v[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r];
-                const size_t o = (size_t)mm * NL + nb;
-                if (nb + 4 <= NL && (NL % 4) == 0) {
-                    if (y_f16) {
-                        const h2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
-                        *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yo) + o) =
-                            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                    for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r];
+                    const size_t o = (size_t)mm * N + nb;
+                    if (nb + 4 <= N && (N % 4) == 0) {
+                        if (y_f16) {
+                            const h2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
+                            *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(Yv) + o) =
+                                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                        } else {
+                            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yv) + o) =
+                                make_float4(v[0], v[1], v[2], v[3]);
+                        }
                     } else {
-                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(Yo) + o) =
-                            make_float4(v[0], v[1], v[2], v[3]);
-                    }
-                } else {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (nb + r >= NL) break;
-                        if (y_f16) reinterpret_cast<_Float16 *>(Yo)[o + r] = (_Float16)v[r];
-                        else reinterpret_cast<float *>(Yo)[o + r] = v[r];
+                        for (int r = 0; r < 4; ++r) {
+                            if (nb + r >= N) break;
+                            if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o + r] = (_Float16)v[r];
+                            else reinterpret_cast<float *>(Yv)[o + r] = v[r];
+                        }
                     }
                 }
             }
@@ -748,11 +776,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 // N = 11008: 19.0 -> 17.7 (2).  Only on the context's own stream (ws.partials
 // is null otherwise); the larger tiles gained nothing from splitting (their
 // LDS rings allow one block per CU).
-// The second member of a weight pair (see k_gemm_rowwise); n_split 0: none.
+// SwiGLU's up weight beside the gate weight of a PAIR launch (see
+// k_gemm_rowwise); n_split = rows of each weight, 0: no pair.
 struct GemmPair {
     const uint8_t *w = nullptr;
     const float *scales = nullptr;
-    void *y = nullptr;
     int64_t n_split = 0;
 };
 
@@ -774,7 +802,7 @@ int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *
         hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * splits)), dim3(64 * NW), 0, s, (const uint8_t *)w.codes,
                            scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m,
                            tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64,
-                           pair.w, pair.scales, pair.y, (int)(pair.n_split ? pair.n_split : N));
+                           pair.w, pair.scales, (int)(pair.n_split ? pair.n_split : N));
     };
     if constexpr (PAIR) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, true>);
     else if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
@@ -841,7 +869,7 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
     // a tile taller than the tokens (rounded up to 64) only multiplies padding:
     // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
     auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
-    if (pair.n_split) {  // a weight pair: the two large tiles only (the caller falls back otherwise)
+    if (pair.n_split) {  // gate and up: the two large tiles only (the caller falls back otherwise)
         if (fills(128, 256))
             return launch_tiled<128, 256, true, 4, 8, 4, 2, true, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, pair);
         if (fills(128, 128))
@@ -863,29 +891,30 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
 // preparation area (context stream only): the scales transposed to
 // [group][row] and/or the activations cast to fp16, a chunk of rows at a time
 // when they do not fit, each chunk then multiplied by the same kernel.
-// Two per-row int8 weights of one input size in one launch (SwiGLU's gate and
-// up): Ya = X . deq(a)^T, Yb = X . deq(b)^T.  Their rows form one grid of
-// a.n_out + b.n_out, so the tile heuristic sees the combined width (at 512
+// SwiGLU's gate and up in one launch with the silu*mul epilogue:
+// h = fp16(silu(g) * u), g = fp16(X . deq(gate)^T), u = fp16(X . deq(up)^T),
+// h fp16 [m][I].  The two weights form one grid of 2 I rows, each tile taking
+// the same rows of both, so the tile heuristic sees the combined width (at 512
 // tokens x 5632 features: 128x256 tiles over both instead of two launches of
-// 128x128 tiles that each leave a third of the CUs idle).  a.n_out must be a
-// multiple of 256 (every tile width), fp16 activations.
-int launch_gemm_pair(const rq_qweight &a, const rq_qweight &b, const void *x, rq_dtype xt, void *ya, void *yb,
-                     rq_dtype yt, int64_t m, int num_cus, const GemmWorkspace &ws, hipStream_t s) {
-    const int64_t K = a.k_in, N = a.n_out + b.n_out;
-    if (a.format != RQ_Q_ROWWISE_I8 || b.format != RQ_Q_ROWWISE_I8 || b.k_in != K || xt != RQ_F16 ||
-        a.n_out % 256 != 0 || K % 64 != 0 || K > (1 << 21) || !aligned(a.codes, 16) || !aligned(b.codes, 16) ||
-        !aligned(x, 16) || m > 0x7fffffff || N > 0x7fffffff)
+// 128x128 tiles that each leave a third of the CUs idle) and g and u never
+// leave the block.  Per-row int8 weights of one shape, fp16 activations,
+// I % 8 == 0; RQ_ERR_UNSUPPORTED otherwise, or when the grid is too small for
+// the two large tiles.
+int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
+                       int num_cus, const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t I = gate.n_out, K = gate.k_in;
+    if (gate.format != RQ_Q_ROWWISE_I8 || up.format != RQ_Q_ROWWISE_I8 || up.n_out != I || up.k_in != K ||
+        xt != RQ_F16 || I % 8 != 0 || K % 64 != 0 || K > (1 << 21) || !aligned(gate.codes, 16) ||
+        !aligned(up.codes, 16) || !aligned(x, 16) || !aligned(h, 16) || m > 0x7fffffff || 2 * I > 0x7fffffff ||
+        128 * I * 2 >= (1ll << 31))
         return RQ_ERR_UNSUPPORTED;
-    if (yt == RQ_F16 ? !aligned(ya, 8) || !aligned(yb, 8) : !aligned(ya, 16) || !aligned(yb, 16))
-        return RQ_ERR_UNSUPPORTED;
-    rq_qweight w = a;
-    w.n_out = N;
+    rq_qweight w = gate;
+    w.n_out = 2 * I;
     GemmPair pair;
-    pair.w = static_cast<const uint8_t *>(b.codes);
-    pair.scales = b.scales;
-    pair.y = yb;
-    pair.n_split = a.n_out;
-    return gemm_tiles(w, a.scales, 0, x, ya, yt, m, num_cus > 0 ? num_cus : 256, ws, s, pair);
+    pair.w = static_cast<const uint8_t *>(up.codes);
+    pair.scales = up.scales;
+    pair.n_split = I;
+    return gemm_tiles(w, gate.scales, 0, x, h, RQ_F16, m, num_cus > 0 ? num_cus : 256, ws, s, pair);
 }
 
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,

@@ -88,13 +88,16 @@ def test_swiglu_prefill_path(ctx, engine):
     assert ok
 
 
-@pytest.mark.parametrize("m,inter,hidden", [(512, 5632, 2048), (640, 1024, 1024), (2048, 11008, 4096)],
-                         ids=["1b_512", "640", "7b_2048"])
-def test_swiglu_prefill_weight_pair(ctx, engine, m, inter, hidden):
-    """Gate and up through one GEMM launch (I a multiple of 256, enough tokens
-    for the large tiles): the pair's rows [0, I) come from the gate weight into
-    g, [I, 2I) from the up weight into u.  h is checked in full; y on sampled
-    rows against the f64 truth (the 7B shape's full truth is too slow here)."""
+@pytest.mark.parametrize("m,inter,hidden", [(512, 5632, 2048), (1000, 2760, 1024), (2048, 11008, 4096)],
+                         ids=["1b_512", "ragged_1000x2760", "7b_2048"])
+def test_swiglu_prefill_fused(ctx, engine, m, inter, hidden):
+    """Gate and up through one GEMM launch with the silu*mul epilogue (enough
+    tokens for the large tiles): each tile multiplies the same rows of both
+    weights and writes h = silu(g) * u.  2760 intermediate rows leave the last
+    tile 72 of its 128 rows per weight and 1000 tokens a partial token tile.
+    h is checked on sampled rows against the f64 truth (with g and u rounded to
+    fp16 as the device rounds them), y likewise (the 7B shape's full truth is
+    too slow here)."""
     g = synth.rng(1000 + m)
     wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
     x = synth.activations(g, m, hidden, sigma=0.5)
@@ -103,13 +106,29 @@ def test_swiglu_prefill_weight_pair(ctx, engine, m, inter, hidden):
     rows = np.unique(np.concatenate([[0, 1, m // 2, m - 2, m - 1], synth.rng(m).integers(0, m, 12)]))
     ht = h_truth(x[rows], wg, sg, wu, su)
     max_abs, rel, ok_h = f16_tol_check(h[rows], ht)
-    print(f"[pair {m}x{inter}x{hidden}] h max_abs={max_abs:.3e}", flush=True)
+    print(f"[fused {m}x{inter}x{hidden}] h max_abs={max_abs:.3e}", flush=True)
     assert ok_h
-    # g and u land in the right halves: a swap or an offset row shows in h everywhere
+    # a swapped gate/up half or an offset row shows in h everywhere
     assert np.isfinite(h).all()
     truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x[rows].astype(np.float32))
     max_abs, rel, ok = f16_tol_check(y[rows], truth)
-    print(f"[pair {m}x{inter}x{hidden}] y max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    print(f"[fused {m}x{inter}x{hidden}] y max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
+def test_swiglu_prefill_fused_128x128(ctx, engine):
+    """1024 tokens x 2 x 2048 rows take the fused epilogue on the 128x128 tile
+    (the cases above run 128x256): h and y against the f64 truth on rows at
+    token-tile edges."""
+    g = synth.rng(4242)
+    m, inter, hidden = 1024, 2048, 1024
+    wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
+    x = synth.activations(g, m, hidden, sigma=0.5)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    rows = np.array([0, 127, 128, 511, 895, 1023])
+    _, _, ok_h = f16_tol_check(h[rows], h_truth(x[rows], wg, sg, wu, su))
+    assert ok_h and np.isfinite(h).all()
+    _, _, ok = f16_tol_check(y[rows], orc.swiglu_truth(wg, sg, wu, su, wd, sd, x[rows].astype(np.float32)))
     assert ok
 
 
