@@ -29,6 +29,12 @@ Printed JSON (one line, stdout):
                    greedy decode steps timed (HIP events), tokens/s; `decode`
                    also holds the batched prefill of that prompt (tokens/s,
                    TFLOPS of its GEMM + attention work) next to the stepwise one
+  ops              the path's other operations, each against its roofline: the
+                   reference's two dequantize kernels (4096^2 elements), its f32
+                   tiled matmul (k-ascending, bit-exact with the reference's order;
+                   configs[0] and 4096^3, the shape the reference publishes:
+                   120.71 GFLOPS on an Apple M2), the frozen-weight input gradient
+                   and Linear::forward with a LoRA adapter
 
 Algorithmic bytes per GEMV = N*K (codes) + 4*N (scales) + 2*M*K (X) + 2*M*N (Y).
 """
@@ -368,6 +374,89 @@ def swiglu(ctx, engine, m: int, copies: int = 4, launches: int = 60, use_graph: 
             "bytes": nbytes, "launches": "gate+up pass, down pass (2 kernels)"}
 
 
+REF_MATMUL_4096_GFLOPS = 120.71  # f32 matmul 4096^3 on an Apple M2, benchmarks/RESULTS.md:21
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 (packed FMA; one-wide VALU FMA issue gives half)
+
+
+def ops_bench(ctx, engine, use_graph: bool = True) -> list:
+    """The path's remaining operations, each timed like the GEMMs (captured,
+    after >= 0.25 s of warm-up replays, median of 3) against its roofline:
+      dequantize          a2, kernels.wgsl:153-166: 1 B read + 4 B written per element
+      affine_dequantize   a1, kernels.wgsl:379-400: + 8 B (scale, bias) per 64 elements
+      matmul_f32          a3, kernels.wgsl:7-54: 2 m k n flops, fp32 VALU
+      qmatmul_dx          f-4, MatMulNode::backward: dX = dY . deq(W), 2 m n k flops, fp32 VALU
+      qmatmul_lora        a7 with an adapter, lib.rs:69-83: the fused product plus (x.A).B
+    The dequantize kernels rotate 8 inputs and 4 outputs (384 MB, past the
+    256 MB Infinity Cache)."""
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+
+    g = synth.rng(5)
+    out = []
+
+    def timed(fn, calls):
+        return sorted(t / calls * 1e3 for t in _replays(ctx, fn, calls, use_graph))[1]  # us per call
+
+    n = 4096 * 4096
+    words = [UnifiedTensor.new(ctx, g.integers(0, 256, n, dtype=np.uint8), dtype=DType.U8) for _ in range(8)]
+    outs = [UnifiedTensor.empty(ctx, [n], DType.FP32) for _ in range(4)]
+    fn = lambda: [engine.dequantize(ctx, words[i], outs[i % 4]) for i in range(8)]  # noqa: E731
+    us = timed(fn, 8)
+    nb = 5 * n
+    out.append({"op": "dequantize", "ref": "kernels.wgsl:153-166", "elements": n, "us": round(us, 2),
+                "bytes": nb, "gbs": round(nb / us / 1e3, 1), "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+    sc = [UnifiedTensor.new(ctx, g.uniform(0.001, 0.02, n // 64).astype(np.float32)) for _ in range(8)]
+    bi = [UnifiedTensor.new(ctx, g.uniform(-2.5, -0.1, n // 64).astype(np.float32)) for _ in range(8)]
+    fn = lambda: [engine.affine_dequantize(ctx, words[i], sc[i], bi[i], outs[i % 4]) for i in range(8)]  # noqa: E731
+    us = timed(fn, 8)
+    nb = 5 * n + 8 * n // 64
+    out.append({"op": "affine_dequantize", "ref": "kernels.wgsl:379-400", "elements": n, "us": round(us, 2),
+                "bytes": nb, "gbs": round(nb / us / 1e3, 1), "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+    del words, outs, sc, bi
+
+    for m, k, nn, calls in ((8, 1024, 1024, 20), (4096, 4096, 4096, 1)):
+        a = UnifiedTensor.new(ctx, g.standard_normal((m, k)).astype(np.float32))
+        b = UnifiedTensor.new(ctx, g.standard_normal((k, nn)).astype(np.float32))
+        c = UnifiedTensor.empty(ctx, [m, nn], DType.FP32)
+        us = timed(lambda: [engine.matmul(ctx, a, b, c) for _ in range(calls)], calls)
+        gf = 2 * m * k * nn / us / 1e3
+        e = {"op": "matmul_f32", "ref": "kernels.wgsl:7-54", "m": m, "k": k, "n": nn, "us": round(us, 2),
+             "gflops": round(gf, 1), "frac_fp32_peak": round(gf / 1e3 / FP32_PEAK_TFLOPS, 4)}
+        if (m, k, nn) == (4096, 4096, 4096):
+            e["vs_published_m2"] = round(gf / REF_MATMUL_4096_GFLOPS, 1)
+        out.append(e)
+        del a, b, c
+
+    w = QuantizedTensor.rowwise(ctx, *synth.rowwise_weight(g, 4096, 4096))
+    m = 512
+    dy = UnifiedTensor.new(ctx, synth.activations(g, m, 4096), dtype=DType.FP16)
+    dx = UnifiedTensor.empty(ctx, [m, 4096], DType.FP32)
+    us = timed(lambda: [engine.qmatmul_dx(ctx, dy, w, dx) for _ in range(4)], 4)
+    gf = 2 * m * 4096 * 4096 / us / 1e3
+    out.append({"op": "qmatmul_dx", "ref": "rusty-autograd/src/lib.rs:152-158", "m": m, "n_out": 4096, "k_in": 4096,
+                "us": round(us, 2), "gflops": round(gf, 1), "frac_fp32_peak": round(gf / 1e3 / FP32_PEAK_TFLOPS, 4)})
+
+    rank = 16
+    la = UnifiedTensor.new(ctx, (g.standard_normal((4096, rank)) * 0.01).astype(np.float32))
+    lb = UnifiedTensor.new(ctx, (g.standard_normal((rank, 4096)) * 0.01).astype(np.float32))
+    for m in (1, 512):
+        x = UnifiedTensor.new(ctx, synth.activations(g, m, 4096), dtype=DType.FP16)
+        y = UnifiedTensor.empty(ctx, [m, 4096], DType.FP16)
+        need = _lora_workspace(m, 4096, 4096, rank)
+        ws = UnifiedTensor.empty(ctx, [need], DType.U8)
+        us = timed(lambda: [engine.qmatmul_lora(ctx, x, w, la, lb, y, ws) for _ in range(4)], 4)
+        base = timed(lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(4)], 4)
+        out.append({"op": "qmatmul_lora", "ref": "rusty-graph/src/lib.rs:69-83", "m": m, "n_out": 4096, "k_in": 4096,
+                    "rank": rank, "us": round(us, 2), "us_without_adapter": round(base, 2),
+                    "what": "y fp16 = x . deq(W)^T + (x . A) . B; the same weight every call (L2/MALL-resident)"})
+    return out
+
+
+def _lora_workspace(m, k, n, rank):
+    from rusty_amd import _lib
+
+    return int(_lib.lib().rq_qmatmul_lora_workspace(m, k, n, rank, 1, 1))
+
+
 def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False) -> dict:
     """1.1B int8 Llama greedy decode, one HIP-graph launch per token.
     Algorithmic bytes per token = int8 codes + f32 scales of every Linear and
@@ -544,7 +633,7 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor", "vendor"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor", "vendor", "ops"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
@@ -580,6 +669,8 @@ def main() -> int:
             out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
         elif args.only == "vendor":
             out["vendor_gemm"] = vendor_gemm()
+        elif args.only == "ops":
+            out["ops"] = ops_bench(ctx, engine, use_graph=not args.no_graph)
         else:
             out["decode"] = decode_loop(ctx, eager=args.decode_eager)
         log(f"{out}")
@@ -650,6 +741,9 @@ def main() -> int:
         result["decode_tok_s"] = dec["tok_s"]
         result["prefill_tok_s"] = dec["prefill"]["tok_s"]
         result["decode"] = dec
+        result["ops"] = ops_bench(ctx, engine)
+        for e in result["ops"]:
+            log(f"op {e}")
 
     if not args.no_cpu_baseline:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")

@@ -97,12 +97,149 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
         }
 }
 
+// Grids of few 64x64 tiles (few rows or few columns: configs[0]'s 8 x 1024,
+// a LoRA adapter's x . A with 16 columns) leave most CUs idle while each
+// block walks all of k alone, 16 k-steps per pair of barriers.  There, a
+// block owns a TR x TC output tile, one output per thread (TR * TC = 256),
+// and the same k-ascending fma chain per output runs over k-chunks of KC
+// staged in LDS by all the block's threads (coalesced along the operand's
+// contiguous dimension); the next chunk's loads are in registers before the
+// current chunk's chains run.  A is staged [TR][KC + 4] (16-byte rows: four
+// k-steps per LDS read), B [KC][TC].
+template <int V, int TC>
+__global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict__ a, const float *__restrict__ b,
+                                                         float *__restrict__ out, int64_t m, int64_t k, int64_t n) {
+    constexpr int TR = TH / TC;
+    constexpr int KC = TC == 16 || TC == 32 ? 512 : 256;  // 64-80 KiB of LDS per chunk
+    constexpr int AS = KC + 4;                       // padded A row (floats)
+    constexpr int NA = TR * KC / TH, NB = KC * TC / TH;  // chunk elements per thread
+    constexpr int G = 32;                            // k-steps per register set of the chains
+    // (+ G: the chains' reads one register set past the chunk stay inside the arrays)
+    __shared__ __attribute__((aligned(16))) float As[TR * AS + G];
+    __shared__ float Bs[(KC + G) * TC];
+    const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
+    const int tr = t / TC, tc = t % TC;  // this thread's output
+    // chunk element e of this thread: A (row, k) and B (k, column) within the chunk
+    auto a_at = [&](int e, int &r, int &kk) {
+        const int i = t + TH * e;
+        if constexpr (V == MM_ATB) { kk = i / TR; r = i % TR; }  // A stored [k, m]: contiguous along rows
+        else { r = i / KC; kk = i % KC; }
+    };
+    auto b_at = [&](int e, int &kk, int &c) {
+        const int i = t + TH * e;
+        if constexpr (V == MM_ABT) { c = i / KC; kk = i % KC; }  // B stored [n, k]: contiguous along k
+        else { kk = i / TC; c = i % TC; }
+    };
+    float ra[NA], rb[NB];
+    auto load = [&](int64_t k0) {
+#pragma unroll
+        for (int e = 0; e < NA; ++e) {
+            int r, kk;
+            a_at(e, r, kk);
+            ra[e] = load_a<V>(a, r0 + r, k0 + kk, m, k);
+        }
+#pragma unroll
+        for (int e = 0; e < NB; ++e) {
+            int kk, c;
+            b_at(e, kk, c);
+            rb[e] = load_b<V>(b, k0 + kk, c0 + c, k, n);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int e = 0; e < NA; ++e) {
+            int r, kk;
+            a_at(e, r, kk);
+            As[r * AS + kk] = ra[e];
+        }
+#pragma unroll
+        for (int e = 0; e < NB; ++e) {
+            int kk, c;
+            b_at(e, kk, c);
+            Bs[kk * TC + c] = rb[e];
+        }
+    };
+    float acc = 0.0f;
+    if (k > 0) load(0);
+    for (int64_t k0 = 0; k0 < k; k0 += KC) {
+        stage();
+        __syncthreads();
+        if (k0 + KC < k) load(k0 + KC);  // in flight while this chunk's chains run
+        const float *ar = As + tr * AS;
+        if (k0 + KC <= k) {
+            // two named register sets of G k-steps: the next set's LDS reads are
+            // issued (unconditionally) before the current set's fmas
+            float xa0[G], xb0[G], xa1[G], xb1[G];
+            auto rd = [&](float *xa, float *xb, int kk) {
+#pragma unroll
+                for (int i = 0; i < G; i += 4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(ar + kk + i);
+                    xa[i] = v.x;
+                    xa[i + 1] = v.y;
+                    xa[i + 2] = v.z;
+                    xa[i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < G; ++i) xb[i] = Bs[(kk + i) * TC + tc];
+            };
+            auto fm = [&](const float *xa, const float *xb) {
+#pragma unroll
+                for (int i = 0; i < G; ++i) acc = __builtin_fmaf(xa[i], xb[i], acc);
+            };
+            rd(xa0, xb0, 0);
+            for (int kk = 0; kk < KC; kk += 2 * G) {
+                rd(xa1, xb1, kk + G);
+                fm(xa0, xb0);
+                rd(xa0, xb0, kk + 2 * G);  // at the chunk's end: read, not used
+                fm(xa1, xb1);
+            }
+        } else {
+            const int kc = (int)(k - k0);
+            for (int kk = 0; kk < kc; ++kk) acc = __builtin_fmaf(ar[kk], Bs[kk * TC + tc], acc);
+        }
+        __syncthreads();  // every chain is done with the chunk before it is overwritten
+    }
+    const int64_t r = r0 + tr, c = c0 + tc;
+    if (r < m && c < n) out[r * n + c] = acc;
+}
+
+template <int V>
+int launch_chain(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n, hipStream_t s) {
+    const int tc = n >= 64 ? 64 : (n > 16 ? 32 : (n > 8 ? 16 : 8));
+    const int64_t gx = cdiv(n, tc), gy = cdiv(m, TH / tc);
+    if (gx > 0x7fffffff || gy > 65535)
+        return fail(RQ_ERR_SHAPE, "matmul grid too large (m=%lld n=%lld)", (long long)m, (long long)n);
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    switch (tc) {
+    case 64: hipLaunchKernelGGL((k_matmul_f32_chain<V, 64>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 32: hipLaunchKernelGGL((k_matmul_f32_chain<V, 32>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 16: hipLaunchKernelGGL((k_matmul_f32_chain<V, 16>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    default: hipLaunchKernelGGL((k_matmul_f32_chain<V, 8>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    }
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
 }  // namespace
 
 int launch_matmul_f32(int variant, const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
                       hipStream_t s) {
     if (m == 0 || n == 0) return RQ_OK;
     const int64_t gx = cdiv(n, BN), gy = cdiv(m, BM);
+    // The chain kernel for few outputs or few tiles, measured (MI355X, us,
+    // chain / tiled, C = A.B): 8x1024x1024 22.8 / 107, 1x4096x16 53 / 404,
+    // 512x4096x16 54 / 465, 16x4096x4096 85 / 581, 64x1024x1024 23 / 118;
+    // with more outputs the tiled kernel's reuse wins (256x1024x4096 346 /
+    // 120; 128x2048x2048 with B transposed 365 / 227).
+    if (m * n <= 65536 || gx * gy < 64) {
+        switch (variant) {
+        case MM_AB: return launch_chain<MM_AB>(a, b, out, m, k, n, s);
+        case MM_ABT: return launch_chain<MM_ABT>(a, b, out, m, k, n, s);
+        case MM_ATB: return launch_chain<MM_ATB>(a, b, out, m, k, n, s);
+        default: return fail(RQ_ERR_INVALID_ARGUMENT, "unknown matmul variant %d", variant);
+        }
+    }
     if (gx > 0x7fffffff || gy > 65535)
         return fail(RQ_ERR_SHAPE, "matmul grid too large (m=%lld n=%lld)", (long long)m, (long long)n);
     const dim3 grid((unsigned)gx, (unsigned)gy), block(TH);

@@ -15,7 +15,14 @@ from rusty_amd import UnifiedTensor
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(2, 2, 2), (1, 1024, 1024), (8, 1024, 1024), (65, 33, 70), (128, 256, 96), (3, 0, 5), (1, 4096, 4096)]
+# Few outputs or few 64x64 tiles take the one-output-per-thread chain kernel
+# (k-chunks of 256 or 512 staged in LDS, column tiles of 8/16/32/64): k past
+# a chunk and not a multiple of 32, k = 0, every column-tile width; the others
+# (512x200x520, 1030x64x600) the 64x64 tiled kernel.  Both must match the
+# oracle bit for bit.
+SHAPES = [(2, 2, 2), (1, 1024, 1024), (8, 1024, 1024), (65, 33, 70), (128, 256, 96), (3, 0, 5), (1, 4096, 4096),
+          (1, 4097, 16), (5, 1000, 40), (33, 600, 9), (7, 300, 3), (2, 513, 100), (512, 4096, 16),
+          (512, 200, 520), (1030, 64, 600)]
 
 
 def _run(engine, ctx, op, a, b, m, n):
