@@ -80,7 +80,20 @@ def test_affine_group_sizes_and_unaligned(ctx, engine):
         assert np.array_equal(bits(got), bits(orc.affine_dequantize(u, s, b, group=group))), group
 
 
-@pytest.mark.parametrize("shape", [(1024, 1024), (4096, 4096), (11008, 4096), (5, 24), (3, 7)])
+@pytest.mark.parametrize("group", [16, 32, 48, 128])
+def test_affine_group_sizes_aligned(ctx, engine, group):
+    """Aligned pointers take the wave-step path (1024 elements per wave step,
+    each lane's 4-element pieces 256 apart): a power-of-two group by shift, 48
+    by division; 9 x 480 elements = 4 full steps + a 224-element tail."""
+    g = synth.rng(300 + group)
+    u, s, b = synth.affine_weight(g, 9, 480, group=group)
+    w = UnifiedTensor.new(ctx, u.ravel(), dtype=DType.U8)
+    out = UnifiedTensor.empty(ctx, [u.size])
+    engine.affine_dequantize(ctx, w, UnifiedTensor.new(ctx, s), UnifiedTensor.new(ctx, b), out, group=group)
+    assert np.array_equal(bits(out.to_vec()), bits(orc.affine_dequantize(u, s, b, group=group))), group
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024), (4096, 4096), (11008, 4096), (5, 24), (3, 7), (3, 1040)])
 def test_rowwise_weight_dequantize_bit_exact(ctx, engine, shape):
     g = synth.rng(shape[0])
     q, s = synth.rowwise_weight(g, *shape)
