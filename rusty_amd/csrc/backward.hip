@@ -22,6 +22,8 @@
 // overlap its arithmetic (a few blocks per CU at prompt-sized m cannot hide
 // the latency by occupancy alone: 512 x 4096 x 4096 took 730 us with
 // single-buffered 16-step tiles).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace rq {
@@ -29,25 +31,25 @@ namespace {
 
 constexpr int BM = 64, BN = 64, BK = 32, TH = 256;
 
-// The dequantized value of code c of weight row `row`, column `col`.
+// The dequantized value of code c with its row's (per-row codes) or group's
+// (affine) scale s and bias b.
 template <int FMT>
-__device__ __forceinline__ float deq1(uint32_t c, const float *scales, const float *biases, int group, int64_t row,
-                                      int64_t col, int64_t k_in) {
+__device__ __forceinline__ float deq1(uint32_t c, float s, float b) {
     if constexpr (FMT == RQ_Q_ROWWISE_I8) {
-        return (float)(int8_t)c * scales[row];
+        return (float)(int8_t)c * s;
     } else {
-        const int64_t g = (row * k_in + col) / group;
         float v;
         {
 #pragma clang fp contract(off)
-            v = (float)c * scales[g];
-            v = v + (biases ? biases[g] : 0.0f);
+            v = (float)c * s;
+            v = v + b;
         }
         return v;
     }
 }
 
-template <int FMT, bool DYF16, bool DXF16>
+// VW: codes 8-byte aligned and k_in % 8 == 0 (8 codes per load).
+template <int FMT, bool DYF16, bool DXF16, bool VW>
 __global__ __launch_bounds__(TH) void k_qmatmul_dx(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
                                                    const float *__restrict__ biases, int group,
                                                    const void *__restrict__ dyv, void *__restrict__ dxv, int64_t m,
@@ -61,44 +63,59 @@ __global__ __launch_bounds__(TH) void k_qmatmul_dx(const uint8_t *__restrict__ c
     // (contiguous along n_out); weight row br of the step, columns bc..bc+7
     const int ar = t / 4, ac = (t % 4) * 8;
     const int br = t / 8, bc = (t % 8) * 8;
-    const bool vec_w = k_in % 8 == 0 && (reinterpret_cast<uintptr_t>(codes) % 8) == 0;
 
-    float ya[8];
-    uint32_t wc[8];
+    // raw loads (an out-of-range element loads element 0 of its operand) and
+    // the zeroing of out-of-range elements at staging: a branch or a select
+    // right after each load made the compiler wait for it before the fmas
+    // raw loads into registers (conversions wait for their loads, so they are
+    // done when staging): dY values as stored, 8 codes as one 8-byte word (or
+    // 8 bytes where codes are unaligned or k_in % 8 != 0), their scales
+    typedef _Float16 yt_t;
+    std::conditional_t<DYF16, yt_t, float> yr[8];
+    uint2 wq;        // VW
+    uint8_t wb8[8];  // !VW
+    float ws[FMT == RQ_Q_ROWWISE_I8 ? 1 : 8], wb[FMT == RQ_Q_ROWWISE_I8 ? 1 : 8];  // scales (and biases)
     auto load = [&](int64_t k0) {
         const int64_t gr = m0 + ar;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t gc = k0 + ac + e;
-            float v = 0.0f;
-            if (gr < m && gc < n_out) {
-                const int64_t o = gr * n_out + gc;
-                v = DYF16 ? (float)static_cast<const _Float16 *>(dyv)[o] : static_cast<const float *>(dyv)[o];
-            }
-            ya[e] = v;
+            const int64_t o = gr < m && gc < n_out ? gr * n_out + gc : 0;
+            if constexpr (DYF16) yr[e] = static_cast<const _Float16 *>(dyv)[o];
+            else yr[e] = static_cast<const float *>(dyv)[o];
         }
         const int64_t row = k0 + br, col = c0 + bc;
-        if (row < n_out && vec_w && col + 8 <= k_in) {
-            const uint2 q = *reinterpret_cast<const uint2 *>(codes + row * k_in + col);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                wc[e] = (q.x >> (8 * e)) & 0xFFu;
-                wc[4 + e] = (q.y >> (8 * e)) & 0xFFu;
-            }
+        if constexpr (VW) {  // k_in % 8 == 0: a thread's 8 columns are all in the row or all past it
+            wq = *reinterpret_cast<const uint2 *>(codes + (row < n_out && col < k_in ? row * k_in + col : 0));
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) wc[e] = row < n_out && col + e < k_in ? codes[row * k_in + col + e] : 0u;
+            for (int e = 0; e < 8; ++e) wb8[e] = codes[row < n_out && col + e < k_in ? row * k_in + col + e : 0];
+        }
+        if constexpr (FMT == RQ_Q_ROWWISE_I8) {
+            ws[0] = scales[row < n_out ? row : 0];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t g = row < n_out && col + e < k_in ? (row * k_in + col + e) / group : 0;
+                ws[e] = scales[g];
+                wb[e] = biases ? biases[g] : 0.0f;
+            }
         }
     };
     auto stage = [&](int64_t k0) {
+        const int64_t gr = m0 + ar;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) As[ac + e][ar] = ya[e];
+        for (int e = 0; e < 8; ++e) As[ac + e][ar] = gr < m && k0 + ac + e < n_out ? (float)yr[e] : 0.0f;
         const int64_t row = k0 + br, col = c0 + bc;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
+        for (int e = 0; e < 8; ++e) {
+            uint32_t c;
+            if constexpr (VW) c = ((e < 4 ? wq.x : wq.y) >> (8 * (e % 4))) & 0xFFu;
+            else c = wb8[e];
             Bs[br][bc + e] = row < n_out && col + e < k_in
-                                 ? deq1<FMT>(wc[e], scales, biases, group, row, col + e, k_in)
+                                 ? deq1<FMT>(c, ws[FMT == RQ_Q_ROWWISE_I8 ? 0 : e], wb[FMT == RQ_Q_ROWWISE_I8 ? 0 : e])
                                  : 0.0f;
+        }
     };
 
     float acc[4][4];
@@ -141,12 +158,13 @@ __global__ __launch_bounds__(TH) void k_qmatmul_dx(const uint8_t *__restrict__ c
 template <int FMT, bool DYF16>
 int launch_fmt(const rq_qweight &w, const void *dy, void *dx, bool dxf16, int64_t m, dim3 grid, hipStream_t s) {
     const uint8_t *codes = static_cast<const uint8_t *>(w.codes);
-    if (dxf16)
-        hipLaunchKernelGGL((k_qmatmul_dx<FMT, DYF16, true>), grid, dim3(TH), 0, s, codes, w.scales, w.biases, w.group,
-                           dy, dx, m, w.n_out, w.k_in);
-    else
-        hipLaunchKernelGGL((k_qmatmul_dx<FMT, DYF16, false>), grid, dim3(TH), 0, s, codes, w.scales, w.biases,
-                           w.group, dy, dx, m, w.n_out, w.k_in);
+    const bool vw = w.k_in % 8 == 0 && aligned(codes, 8);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(TH), 0, s, codes, w.scales, w.biases, w.group, dy, dx, m, w.n_out,
+                           w.k_in);
+    };
+    if (dxf16) vw ? go(k_qmatmul_dx<FMT, DYF16, true, true>) : go(k_qmatmul_dx<FMT, DYF16, true, false>);
+    else vw ? go(k_qmatmul_dx<FMT, DYF16, false, true>) : go(k_qmatmul_dx<FMT, DYF16, false, false>);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }

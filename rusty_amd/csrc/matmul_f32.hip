@@ -19,20 +19,25 @@ namespace {
 
 constexpr int BM = 64, BN = 64, BK = 16, TH = 256;
 
+// Operand loads without branches or selects on the loaded value: an
+// out-of-range element loads element 0 (the callers never load from an empty
+// operand) and is replaced by zero only when it is staged, after the loads of
+// a whole step are in flight.  A branch around each load made the compiler
+// wait for every load at its join (s_waitcnt vmcnt(0) per element), and a
+// select right after the load waits for it just the same.
+// logical A[r, c] with r < m, c < k; A stored [k, m] for MM_ATB
 template <int V>
-__device__ __forceinline__ float load_a(const float *a, int64_t r, int64_t c, int64_t m, int64_t k) {
-    // logical A[r, c] with r < m, c < k
-    if (r >= m || c >= k) return 0.0f;
-    if constexpr (V == MM_ATB) return a[c * m + r];  // A stored [k, m]
-    else return a[r * k + c];
+__device__ __forceinline__ bool in_a(int64_t r, int64_t c, int64_t m, int64_t k) { return r < m && c < k; }
+template <int V>
+__device__ __forceinline__ float raw_a(const float *a, int64_t r, int64_t c, int64_t m, int64_t k) {
+    return a[in_a<V>(r, c, m, k) ? (V == MM_ATB ? c * m + r : r * k + c) : 0];
 }
-
+// logical B[r, c] with r < k, c < n; B stored [n, k] for MM_ABT
 template <int V>
-__device__ __forceinline__ float load_b(const float *b, int64_t r, int64_t c, int64_t k, int64_t n) {
-    // logical B[r, c] with r < k, c < n
-    if (r >= k || c >= n) return 0.0f;
-    if constexpr (V == MM_ABT) return b[c * k + r];  // B stored [n, k]
-    else return b[r * n + c];
+__device__ __forceinline__ bool in_b(int64_t r, int64_t c, int64_t k, int64_t n) { return r < k && c < n; }
+template <int V>
+__device__ __forceinline__ float raw_b(const float *b, int64_t r, int64_t c, int64_t k, int64_t n) {
+    return b[in_b<V>(r, c, k, n) ? (V == MM_ABT ? c * k + r : r * n + c) : 0];
 }
 
 template <int V>
@@ -50,30 +55,46 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
 
-    for (int64_t k0 = 0; k0 < k; k0 += BK) {
-        // A tile: BM x BK.  Coalesce along the contiguous dimension.
+    // A tile BM x BK and B tile BK x BN, each thread's 4 + 4 elements coalesced
+    // along the operand's contiguous dimension; the next step's elements are
+    // loaded into registers before the current step's fmas run (all of them
+    // in flight at once: stored to LDS one by one as they arrived, each load
+    // had waited for the previous one).
+    float ra[4], rb[4];
+    auto a_at = [&](int i, int &r, int &c) {
+        if constexpr (V == MM_ATB) { r = t % 64; c = t / 64 + 4 * i; }
+        else { c = t % 16; r = t / 16 + 16 * i; }
+    };
+    auto b_at = [&](int i, int &r, int &c) {  // r: k within the step, c: column
+        if constexpr (V == MM_ABT) { r = t % 16; c = t / 16 + 16 * i; }
+        else { c = t % 64; r = t / 64 + 4 * i; }
+    };
+    auto load = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if constexpr (V == MM_ATB) {
-                const int r = t % 64, c = t / 64 + 4 * i;
-                As[c][r] = load_a<V>(a, m0 + r, k0 + c, m, k);
-            } else {
-                const int c = t % 16, r = t / 16 + 16 * i;
-                As[c][r] = load_a<V>(a, m0 + r, k0 + c, m, k);
-            }
+            int r, c;
+            a_at(i, r, c);
+            ra[i] = raw_a<V>(a, m0 + r, k0 + c, m, k);
         }
-        // B tile: BK x BN.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if constexpr (V == MM_ABT) {
-                const int c = t % 16, r = t / 16 + 16 * i;
-                Bs[c][r] = load_b<V>(b, k0 + c, n0 + r, k, n);
-            } else {
-                const int r = t % 64, c = t / 64 + 4 * i;
-                Bs[c][r] = load_b<V>(b, k0 + c, n0 + r, k, n);
-            }
+            int r, c;
+            b_at(i, r, c);
+            rb[i] = raw_b<V>(b, k0 + r, n0 + c, k, n);
+        }
+    };
+    if (k > 0) load(0);
+    for (int64_t k0 = 0; k0 < k; k0 += BK) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int r, c;
+            a_at(i, r, c);
+            As[c][r] = in_a<V>(m0 + r, k0 + c, m, k) ? ra[i] : 0.0f;
+            b_at(i, r, c);
+            Bs[r][c] = in_b<V>(k0 + r, n0 + c, k, n) ? rb[i] : 0.0f;
         }
         __syncthreads();
+        if (k0 + BK < k) load(k0 + BK);
 #pragma unroll
         for (int kk = 0; kk < BK; ++kk) {
             float av[4], bv[4];
@@ -104,8 +125,8 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
 // and the same k-ascending fma chain per output runs over k-chunks of KC
 // staged in LDS by all the block's threads (coalesced along the operand's
 // contiguous dimension); the next chunk's loads are in registers before the
-// current chunk's chains run.  A is staged [TR][KC + 4] (16-byte rows: four
-// k-steps per LDS read), B [KC][TC].
+// current chunk's chains run.  A is staged [TR][KC + 4] and B transposed,
+// [TC][KC + 4] (16-byte rows: four k-steps of each operand per LDS read).
 template <int V, int TC>
 __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict__ a, const float *__restrict__ b,
                                                          float *__restrict__ out, int64_t m, int64_t k, int64_t n) {
@@ -116,7 +137,7 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     constexpr int G = 32;                            // k-steps per register set of the chains
     // (+ G: the chains' reads one register set past the chunk stay inside the arrays)
     __shared__ __attribute__((aligned(16))) float As[TR * AS + G];
-    __shared__ float Bs[(KC + G) * TC];
+    __shared__ __attribute__((aligned(16))) float Bs[TC * AS + G];
     const int t = threadIdx.x;
     const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
     const int tr = t / TC, tc = t % TC;  // this thread's output
@@ -137,36 +158,36 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
         for (int e = 0; e < NA; ++e) {
             int r, kk;
             a_at(e, r, kk);
-            ra[e] = load_a<V>(a, r0 + r, k0 + kk, m, k);
+            ra[e] = raw_a<V>(a, r0 + r, k0 + kk, m, k);
         }
 #pragma unroll
         for (int e = 0; e < NB; ++e) {
             int kk, c;
             b_at(e, kk, c);
-            rb[e] = load_b<V>(b, k0 + kk, c0 + c, k, n);
+            rb[e] = raw_b<V>(b, k0 + kk, c0 + c, k, n);
         }
     };
-    auto stage = [&]() {
+    auto stage = [&](int64_t k0) {
 #pragma unroll
         for (int e = 0; e < NA; ++e) {
             int r, kk;
             a_at(e, r, kk);
-            As[r * AS + kk] = ra[e];
+            As[r * AS + kk] = in_a<V>(r0 + r, k0 + kk, m, k) ? ra[e] : 0.0f;
         }
 #pragma unroll
         for (int e = 0; e < NB; ++e) {
             int kk, c;
             b_at(e, kk, c);
-            Bs[kk * TC + c] = rb[e];
+            Bs[c * AS + kk] = in_b<V>(k0 + kk, c0 + c, k, n) ? rb[e] : 0.0f;
         }
     };
     float acc = 0.0f;
     if (k > 0) load(0);
     for (int64_t k0 = 0; k0 < k; k0 += KC) {
-        stage();
+        stage(k0);
         __syncthreads();
         if (k0 + KC < k) load(k0 + KC);  // in flight while this chunk's chains run
-        const float *ar = As + tr * AS;
+        const float *ar = As + tr * AS, *bc = Bs + tc * AS;
         if (k0 + KC <= k) {
             // two named register sets of G k-steps: the next set's LDS reads are
             // issued (unconditionally) before the current set's fmas
@@ -175,13 +196,16 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
 #pragma unroll
                 for (int i = 0; i < G; i += 4) {
                     const float4 v = *reinterpret_cast<const float4 *>(ar + kk + i);
+                    const float4 u = *reinterpret_cast<const float4 *>(bc + kk + i);
                     xa[i] = v.x;
                     xa[i + 1] = v.y;
                     xa[i + 2] = v.z;
                     xa[i + 3] = v.w;
+                    xb[i] = u.x;
+                    xb[i + 1] = u.y;
+                    xb[i + 2] = u.z;
+                    xb[i + 3] = u.w;
                 }
-#pragma unroll
-                for (int i = 0; i < G; ++i) xb[i] = Bs[(kk + i) * TC + tc];
             };
             auto fm = [&](const float *xa, const float *xb) {
 #pragma unroll
@@ -196,7 +220,7 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
             }
         } else {
             const int kc = (int)(k - k0);
-            for (int kk = 0; kk < kc; ++kk) acc = __builtin_fmaf(ar[kk], Bs[kk * TC + tc], acc);
+            for (int kk = 0; kk < kc; ++kk) acc = __builtin_fmaf(ar[kk], bc[kk], acc);
         }
         __syncthreads();  // every chain is done with the chunk before it is overwritten
     }
@@ -227,12 +251,12 @@ int launch_matmul_f32(int variant, const float *a, const float *b, float *out, i
                       hipStream_t s) {
     if (m == 0 || n == 0) return RQ_OK;
     const int64_t gx = cdiv(n, BN), gy = cdiv(m, BM);
-    // The chain kernel for few outputs or few tiles, measured (MI355X, us,
-    // chain / tiled, C = A.B): 8x1024x1024 22.8 / 107, 1x4096x16 53 / 404,
-    // 512x4096x16 54 / 465, 16x4096x4096 85 / 581, 64x1024x1024 23 / 118;
-    // with more outputs the tiled kernel's reuse wins (256x1024x4096 346 /
-    // 120; 128x2048x2048 with B transposed 365 / 227).
-    if (m * n <= 65536 || gx * gy < 64) {
+    // The chain kernel for few outputs or few tiles with more than a few
+    // k-steps, measured (MI355X, us, chain / tiled, C = A.B): 8x1024x1024
+    // 23.5 / 86, 1x4096x16 45 / 335, 16x4096x4096 88 / 342, 64x1024x1024
+    // 24 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
+    // 356 / 88, 512^3 48 / 45), and at k = 16 its one step (1x16x4096 6.2 / 3.3).
+    if (k > 64 && (m * n <= 65536 || gx * gy < 64)) {
         switch (variant) {
         case MM_AB: return launch_chain<MM_AB>(a, b, out, m, k, n, s);
         case MM_ABT: return launch_chain<MM_ABT>(a, b, out, m, k, n, s);
