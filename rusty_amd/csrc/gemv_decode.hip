@@ -202,8 +202,59 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             }
         }
     }
-    // Weight chunks: R rows x CPT chunks per thread, all in flight.
     const int rows_here = min(ROWS, N - row0);
+    // Per-row scales of the tasks this wave will finish, requested before the
+    // weights (and above the prologue's barriers, which the compiler does not
+    // move loads across) so the epilogue does not wait on a global load after
+    // the reduction; issued after the weights, they made the prologue's waits
+    // for its activation row count the weight loads too.
+    constexpr int NTW = (TASKS + DT / 64 - 1) / (DT / 64);  // tasks per wave
+    float srow[NTW], srow2[SWI ? NTW : 1];
+    if constexpr (FMT == 0) {
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            const int rin = (wave + (DT / 64) * i) / M;
+            const bool ok = wave + (DT / 64) * i < TASKS && rin < rows_here;
+            srow[i] = ok ? scales[row0 + rin] : 0.0f;
+            if constexpr (SWI) srow2[i] = ok ? scales2[row0 + rin] : 0.0f;
+        }
+    }
+    // y += result: the old values of the residual, requested now for the same reason
+    float yold[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) {
+        const int task = wave + (DT / 64) * i, rin = task / M, m = task % M;
+        yold[i] = (ymode == kYAdd && task < TASKS && rin < rows_here && m < m_act)
+                      ? reinterpret_cast<const float *>(Yv)[(size_t)m * N + row0 + rin]
+                      : 0.0f;
+    }
+    // Affine: the group scale and bias of every chunk (group % 16 == 0 and
+    // K % group == 0, so a chunk sits in one group: row * (K / group) + c * 16 / group).
+    float sg[NR][CPT], bg[NR][CPT];
+    if constexpr (FMT == 1) {
+        const int gk = K / group;
+        int cg[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) cg[j] = (int)((unsigned)(tt + TPR * j) * 16u / (unsigned)group);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float *sp = r < R ? scales : scales2, *bp = r < R ? biases : biases2;
+            const int rin = (r % R) * RP + rp;
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int c = tt + TPR * j;
+                sg[r][j] = 0.0f;
+                bg[r][j] = 0.0f;
+                if (c < C && rin < rows_here) {
+                    const size_t g = (size_t)(row0 + rin) * gk + cg[j];
+                    sg[r][j] = sp[g];
+                    bg[r][j] = bp ? bp[g] : 0.0f;
+                }
+            }
+        }
+    }
+
+    // Weight chunks: R rows x CPT chunks per thread, all in flight.
     const auto rw = make_rsrc(W + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
     uint4 w[NR][CPT];
@@ -316,54 +367,6 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             xh[j][0][4] = b.x; xh[j][0][5] = b.y; xh[j][0][6] = b.z; xh[j][0][7] = b.w;
         }
     }
-    // Per-row scales of the tasks this wave will finish, requested now so the
-    // epilogue does not wait on a global load after the reduction.
-    constexpr int NTW = (TASKS + DT / 64 - 1) / (DT / 64);  // tasks per wave
-    float srow[NTW], srow2[SWI ? NTW : 1];
-    if constexpr (FMT == 0) {
-#pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-            const int rin = (wave + (DT / 64) * i) / M;
-            const bool ok = wave + (DT / 64) * i < TASKS && rin < rows_here;
-            srow[i] = ok ? scales[row0 + rin] : 0.0f;
-            if constexpr (SWI) srow2[i] = ok ? scales2[row0 + rin] : 0.0f;
-        }
-    }
-    // y += result: the old values of the residual, requested now for the same reason
-    float yold[NTW];
-#pragma unroll
-    for (int i = 0; i < NTW; ++i) {
-        const int task = wave + (DT / 64) * i, rin = task / M, m = task % M;
-        yold[i] = (ymode == kYAdd && task < TASKS && rin < rows_here && m < m_act)
-                      ? reinterpret_cast<const float *>(Yv)[(size_t)m * N + row0 + rin]
-                      : 0.0f;
-    }
-    // Affine: the group scale and bias of every chunk (group % 16 == 0 and
-    // K % group == 0, so a chunk sits in one group: row * (K / group) + c * 16 / group).
-    float sg[NR][CPT], bg[NR][CPT];
-    if constexpr (FMT == 1) {
-        const int gk = K / group;
-        int cg[CPT];
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) cg[j] = (int)((unsigned)(tt + TPR * j) * 16u / (unsigned)group);
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const float *sp = r < R ? scales : scales2, *bp = r < R ? biases : biases2;
-            const int rin = (r % R) * RP + rp;
-#pragma unroll
-            for (int j = 0; j < CPT; ++j) {
-                const int c = tt + TPR * j;
-                sg[r][j] = 0.0f;
-                bg[r][j] = 0.0f;
-                if (c < C && rin < rows_here) {
-                    const size_t g = (size_t)(row0 + rin) * gk + cg[j];
-                    sg[r][j] = sp[g];
-                    bg[r][j] = bp ? bp[g] : 0.0f;
-                }
-            }
-        }
-    }
-
     // Per-chunk sums of X (fp16 dot with (1,1)); zero for chunks past K.
     float xs[CPT][M], xs_tot[M];
 #pragma unroll

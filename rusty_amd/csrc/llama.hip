@@ -202,15 +202,21 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     const float *q = qkv + (size_t)hd * HD;
     const float *k = qkv + (size_t)n_heads * HD + (size_t)g * HD;
     const float *v = qkv + (size_t)(n_heads + n_kv) * HD + (size_t)g * HD;
-    if (t < HALF) {
-        const float2 cs = rope[(size_t)pos * HALF + t];  // (cos, sin) of pos * theta^(-2t/HD)
-        const float q1 = q[t], q2 = q[t + HALF], k1 = k[t], k2 = k[t + HALF];
-        qs[t] = q1 * cs.x - q2 * cs.y;
-        qs[t + HALF] = q1 * cs.y + q2 * cs.x;
-        kn[t] = (float)(_Float16)(k1 * cs.x - k2 * cs.y);
-        kn[t + HALF] = (float)(_Float16)(k1 * cs.y + k2 * cs.x);
+    // this position's q, k, v and RoPE factors, all requested before any is
+    // used (one round trip: a separate branch for v waited for the others
+    // first, a second round trip on the block's critical path)
+    if (t < HD) {
+        const int d = t % HALF;
+        const float2 cs = rope[(size_t)pos * HALF + d];  // (cos, sin) of pos * theta^(-2d/HD)
+        const float q1 = q[d], q2 = q[d + HALF], k1 = k[d], k2 = k[d + HALF], vv = v[t];
+        if (t < HALF) {
+            qs[t] = q1 * cs.x - q2 * cs.y;
+            qs[t + HALF] = q1 * cs.y + q2 * cs.x;
+            kn[t] = (float)(_Float16)(k1 * cs.x - k2 * cs.y);
+            kn[t + HALF] = (float)(_Float16)(k1 * cs.y + k2 * cs.x);
+        }
+        vn[t] = (float)(_Float16)vv;
     }
-    if (t < HD) vn[t] = (float)(_Float16)v[t];
     __syncthreads();
     if (hd % grp == 0 && r1 == T && r0 < r1 && t < HD) {
         kcg[(size_t)pos * HD + t] = (_Float16)kn[t];
