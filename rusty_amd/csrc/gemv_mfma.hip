@@ -150,6 +150,21 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     const int fr = lane % 16, q = lane / 16;  // MFMA operand row (weight row / token) and lane group
     const int n0 = blockIdx.x * RB;
     const int rows_here = min(RB, N - n0);
+    // The row scales of this lane's outputs (rows 4 q + r), requested with the
+    // first weight batch (below): loaded in the epilogue, each output waited
+    // for its scale after the reduction (a round trip per output row on the
+    // block's tail).
+    float sc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sc2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto load_scales = [&]() {
+        if constexpr (FMT == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int f = 4 * q + r, row = n0 + (f < rows_here ? f : 0);
+                sc[r] = scales[row];
+                if constexpr (SWI) sc2[r] = scales2[row];
+            }
+        }
+    };
     const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * (XF ? 4u : 2u));
@@ -294,6 +309,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     Batch<FMT, XF> A, B;
     if (mb > 0) {
         load(A, wave);
+        load_scales();
         int b = 0;
         for (; b + 2 < mb; b += 2) {
             load(B, wave + (b + 1) * NWV);
@@ -337,7 +353,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
                 for (int r = 0; r < 4; ++r) {
                     const int f = 4 * q + r;
                     if (f < rows_here) {
-                        const float h = FMT == 1 ? silu(v[r]) * u[r] : silu(v[r] * scales[n0 + f]) * (u[r] * scales2[n0 + f]);
+                        const float h = FMT == 1 ? silu(v[r]) * u[r] : silu(v[r] * sc[r]) * (u[r] * sc2[r]);
                         reinterpret_cast<_Float16 *>(Yv)[(size_t)m * N + n0 + f] = (_Float16)h;
                     }
                 }
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             for (int r = 0; r < 4; ++r) {
                 const int f = 4 * q + r;
                 if (f < rows_here) {
-                    const float y = FMT == 1 ? v[r] : v[r] * scales[n0 + f];
+                    const float y = FMT == 1 ? v[r] : v[r] * sc[r];
                     const size_t o = (size_t)m * N + n0 + f;
                     if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
                     else reinterpret_cast<float *>(Yv)[o] = y;
