@@ -329,6 +329,29 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    // The per-feature scales of the outputs this wave finishes (feature tile i
+    // = KG io + kg, features fl + r of each 8-row group g), requested before
+    // the k loop: loaded by the epilogue, they cost a round trip on every
+    // block's tail.  Past the weight's rows: a valid row, zeroed at use.
+    constexpr int FNO = FN / KG;
+    auto feat = [&](int io, int g) { return wn * TN + (KG * io + kg) * 32 + 8 * g + h * 4; };
+    auto wrow = [&](int fl) { return nw0 + (PAIR && fl >= HB ? fl - HB : fl); };
+    float esc[FNO][4][4];
+    if constexpr (FMT == 0) {
+#pragma unroll
+        for (int io = 0; io < FNO; ++io)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int fl = feat(io, g);
+                const float *__restrict__ scl = PAIR && fl >= HB ? scalesb : scales;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int wr = wrow(fl) + r;
+                    esc[io][g][r] = scl[wr < NL ? wr : 0];
+                }
+            }
+    }
+
     // A k-step's fragments: raw int8 W (expanded just before the MFMA) and fp16 X.
     // W2 reads a lane's W as one 16-byte piece covering both of its k16 slices
     // (a k permutation: slice kl takes bytes 8 kl .. 8 kl + 7 of the piece at
@@ -661,16 +684,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
             if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
+            const int io = i / KG;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int fl = wn * TN + i * 32 + 8 * g + h * 4;  // feature within the tile
-                // its weight row and scales (PAIR: wave-uniform choice of gate or up)
-                const bool upc = PAIR && fl >= HB;
-                const int wr = nw0 + (upc ? fl - HB : fl);
-                const float *__restrict__ scl = upc ? scalesb : scales;
+                const int fl = feat(io, g);  // feature within the tile
+                const int wr = wrow(fl);     // its weight row (PAIR: of the gate or the up weight)
                 float sc[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[r] = wr + r < NL ? (FMT == 0 ? scl[wr + r] : 1.0f) : 0.0f;
+                for (int r = 0; r < 4; ++r) sc[r] = wr + r < NL ? (FMT == 0 ? esc[io][g][r] : 1.0f) : 0.0f;
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
@@ -729,12 +750,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
             if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
+            const int io = i / KG;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int nb = n0 + wn * TN + i * 32 + 8 * g + h * 4;  // weight row
+                const int nb = n0 + feat(io, g);  // weight row
                 float sc[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? (FMT == 0 ? scales[nb + r] : 1.0f) : 0.0f;
+                for (int r = 0; r < 4; ++r) sc[r] = nb + r < N ? (FMT == 0 ? esc[io][g][r] : 1.0f) : 0.0f;
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     const int mm = m0 + wm * TM + j * 32 + fr;
