@@ -242,14 +242,13 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             const int rin = (r % R) * RP + rp;
 #pragma unroll
             for (int j = 0; j < CPT; ++j) {
+                // branch-free (a branch around each load made every one wait
+                // for the previous): a chunk past K multiplies zero activations
+                // and a row past N is not stored, so those take group 0's values
                 const int c = tt + TPR * j;
-                sg[r][j] = 0.0f;
-                bg[r][j] = 0.0f;
-                if (c < C && rin < rows_here) {
-                    const size_t g = (size_t)(row0 + rin) * gk + cg[j];
-                    sg[r][j] = sp[g];
-                    bg[r][j] = bp ? bp[g] : 0.0f;
-                }
+                const size_t g = c < C && rin < rows_here ? (size_t)(row0 + rin) * gk + cg[j] : 0;
+                sg[r][j] = sp[g];
+                bg[r][j] = bp ? bp[g] : 0.0f;
             }
         }
     }
