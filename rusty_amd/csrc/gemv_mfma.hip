@@ -7,7 +7,8 @@
 // so the products go to v_mfma_f32_16x16x32_f16 (16 features x 16 tokens x 32
 // k per instruction; MFMA throughput is far from the limit here):
 //  * One block of NWV waves per 16 weight rows (SwiGLU: 8 gate + the same 8
-//    up rows).  Wave w takes the 256-k batches w, w + NWV, ...
+//    up rows).  Wave w takes the 256-k batches w, w + NWV, ..., counted from
+//    a per-block rotation that staggers the blocks' activation reads.
 //  * Weights are loaded as 4 rows x 256 contiguous bytes per instruction
 //    (lane chunk lane % 16 of row 4 i + lane / 16): against loading the MFMA
 //    operand layout directly (16 rows x 64 B per instruction) the weight
@@ -175,10 +176,21 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     const uint32_t xbase = ((uint32_t)fr * (uint32_t)K + 8u * (uint32_t)q) * (XF ? 4u : 2u);
     uint8_t *wl = wt[wave];
     const int nb = (K + 255) / 256;  // 256-k batches; wave w takes batches w, w + NWV, ...
+    // ... counted from this block's rotation brot (mod nb).  Every block reads
+    // all of X: unrotated, the blocks that share an XCD's L2 (consecutive
+    // blocks go to the 8 XCDs in turn) all requested the same activation lines
+    // at the same moment.  Block b is the (b / 8)-th of XCD b % 8; stepping the
+    // rotation by 5 per block of an XCD and by 1 per XCD spreads them (MI355X,
+    // us, unrotated -> rotated: m = 4 4096^2 6.41 -> 5.70, m = 16 8.03 -> 7.34,
+    // m = 8 11008x4096 13.63 -> 12.70, m = 8 4096x11008 12.45 -> 11.30; with
+    // X's loads taken out, 5.65 at every m).
+    const int brot = (int)((blockIdx.x >> 3) * 5u + (blockIdx.x & 7u)) % nb;
 
     const int Gpr = K / 64;  // affine groups per row
     auto load = [&](Batch<FMT, XF> &b, int bi) {
-        const uint32_t k0 = (uint32_t)bi * 256u;
+        int bb = bi + brot;
+        bb -= bb >= nb ? nb : 0;
+        const uint32_t k0 = (uint32_t)bb * 256u;
         const bool klive = k0 + 16u * (uint32_t)fr < (uint32_t)K;  // K % 16 == 0
         if constexpr (FMT == 1 && XF) {
             // output rows 4 q + r (SwiGLU: rows 0-7 gate, 8-15 up), four groups each
