@@ -127,11 +127,34 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
 // contiguous dimension); the next chunk's loads are in registers before the
 // current chunk's chains run.  A is staged [TR][KC + 4] and B transposed,
 // [TC][KC + 4] (16-byte rows: four k-steps of each operand per LDS read).
+//
+// The chunk loads are buffer loads at one per-thread 32-bit offset per
+// operand plus a per-element stride held in scalar registers, with no bounds
+// test: a position past the operand reads as zero (the buffer's size), and
+// one past a row's end lands on a value of a row or column whose output is
+// never stored, or on k past K, which no chain reads (a partial chunk's
+// chains stop at K).  Per-element 64-bit addresses with clamped indices kept
+// some 130 VGPRs live across the chunk loop, and the compiler moved the
+// arriving values into AGPRs before the chains -- a wait for the loads it
+// had just issued, so every chunk paid a memory round trip (1 x 4096 x 16:
+// 45 us).  The host keeps every offset below 2^32 (chain_fits).  Waves whose
+// rows all lie past m skip the chains (m = 1 with 16 rows per block: 3 of 4).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+template <int TC>
+constexpr int chain_kc() { return TC == 16 || TC == 32 ? 512 : 256; }  // 64-80 KiB of LDS per chunk
+
 template <int V, int TC>
 __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict__ a, const float *__restrict__ b,
                                                          float *__restrict__ out, int64_t m, int64_t k, int64_t n) {
     constexpr int TR = TH / TC;
-    constexpr int KC = TC == 16 || TC == 32 ? 512 : 256;  // 64-80 KiB of LDS per chunk
+    constexpr int KC = chain_kc<TC>();
+    constexpr int P = KC / TH;                       // chunk rows of TH elements per contiguous row piece
     constexpr int AS = KC + 4;                       // padded A row (floats)
     constexpr int NA = TR * KC / TH, NB = KC * TC / TH;  // chunk elements per thread
     constexpr int G = 32;                            // k-steps per register set of the chains
@@ -139,58 +162,74 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     __shared__ __attribute__((aligned(16))) float As[TR * AS + G];
     __shared__ __attribute__((aligned(16))) float Bs[TC * AS + G];
     const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
     const int tr = t / TC, tc = t % TC;  // this thread's output
-    // chunk element e of this thread: A (row, k) and B (k, column) within the chunk
-    auto a_at = [&](int e, int &r, int &kk) {
-        const int i = t + TH * e;
-        if constexpr (V == MM_ATB) { kk = i / TR; r = i % TR; }  // A stored [k, m]: contiguous along rows
-        else { r = i / KC; kk = i % KC; }
+    const uint32_t K = (uint32_t)k, M = (uint32_t)m, N = (uint32_t)n;
+    const auto ra_ = make_rsrc(a, (uint32_t)(m * k * 4)), rb_ = make_rsrc(b, (uint32_t)(k * n * 4));
+    // Element e of this thread in a chunk: LDS index and byte offset from the
+    // thread's base offset (uniform per e); the bases advance by a chunk.
+    //  A [m, k] (A [k, m] for MM_ATB), B [k, n] (B [n, k] for MM_ABT).
+    uint32_t va, vb, da, db;
+    if constexpr (V == MM_ATB) {
+        va = ((uint32_t)(t / TR) * M + (uint32_t)r0 + (uint32_t)(t % TR)) * 4u;
+        da = (uint32_t)KC * M * 4u;
+    } else {
+        va = ((uint32_t)r0 * K + (uint32_t)t) * 4u;
+        da = (uint32_t)KC * 4u;
+    }
+    if constexpr (V == MM_ABT) {
+        vb = ((uint32_t)c0 * K + (uint32_t)t) * 4u;
+        db = (uint32_t)KC * 4u;
+    } else {
+        vb = ((uint32_t)(t / TC) * N + (uint32_t)c0 + (uint32_t)(t % TC)) * 4u;
+        db = (uint32_t)KC * N * 4u;
+    }
+    auto a_soff = [&](int e) -> uint32_t {
+        if constexpr (V == MM_ATB) return (uint32_t)(TC * e) * M * 4u;
+        else return (uint32_t)(e / P) * K * 4u + (uint32_t)(e % P) * (TH * 4u);
     };
-    auto b_at = [&](int e, int &kk, int &c) {
-        const int i = t + TH * e;
-        if constexpr (V == MM_ABT) { c = i / KC; kk = i % KC; }  // B stored [n, k]: contiguous along k
-        else { kk = i / TC; c = i % TC; }
+    auto a_lds = [&](int e) {
+        if constexpr (V == MM_ATB) return (t % TR) * AS + t / TR + TC * e;
+        else return (e / P) * AS + t + TH * (e % P);
+    };
+    auto b_soff = [&](int e) -> uint32_t {
+        if constexpr (V == MM_ABT) return (uint32_t)(e / P) * K * 4u + (uint32_t)(e % P) * (TH * 4u);
+        else return (uint32_t)(TR * e) * N * 4u;
+    };
+    auto b_lds = [&](int e) {
+        if constexpr (V == MM_ABT) return (e / P) * AS + t + TH * (e % P);
+        else return (t % TC) * AS + t / TC + TR * e;
     };
     float ra[NA], rb[NB];
-    auto load = [&](int64_t k0) {
+    auto load = [&]() {
 #pragma unroll
-        for (int e = 0; e < NA; ++e) {
-            int r, kk;
-            a_at(e, r, kk);
-            ra[e] = raw_a<V>(a, r0 + r, k0 + kk, m, k);
-        }
+        for (int e = 0; e < NA; ++e) ra[e] = bload(ra_, va, a_soff(e));
 #pragma unroll
-        for (int e = 0; e < NB; ++e) {
-            int kk, c;
-            b_at(e, kk, c);
-            rb[e] = raw_b<V>(b, k0 + kk, c0 + c, k, n);
-        }
+        for (int e = 0; e < NB; ++e) rb[e] = bload(rb_, vb, b_soff(e));
+        va += da;
+        vb += db;
     };
-    auto stage = [&](int64_t k0) {
+    auto stage = [&]() {
 #pragma unroll
-        for (int e = 0; e < NA; ++e) {
-            int r, kk;
-            a_at(e, r, kk);
-            As[r * AS + kk] = in_a<V>(r0 + r, k0 + kk, m, k) ? ra[e] : 0.0f;
-        }
+        for (int e = 0; e < NA; ++e) As[a_lds(e)] = ra[e];
 #pragma unroll
-        for (int e = 0; e < NB; ++e) {
-            int kk, c;
-            b_at(e, kk, c);
-            Bs[c * AS + kk] = in_b<V>(k0 + kk, c0 + c, k, n) ? rb[e] : 0.0f;
-        }
+        for (int e = 0; e < NB; ++e) Bs[b_lds(e)] = rb[e];
     };
+    // this wave's rows: (64 / TC) from 64 wave / TC
+    const bool idle = r0 + 64 * wave / TC >= m;
     float acc = 0.0f;
-    if (k > 0) load(0);
+    if (k > 0) load();
     for (int64_t k0 = 0; k0 < k; k0 += KC) {
-        stage(k0);
+        stage();
         __syncthreads();
-        if (k0 + KC < k) load(k0 + KC);  // in flight while this chunk's chains run
+        if (k0 + KC < k) load();  // in flight while this chunk's chains run
         const float *ar = As + tr * AS, *bc = Bs + tc * AS;
-        if (k0 + KC <= k) {
+        if (idle) {
+        } else if (k0 + KC <= k) {
             // two named register sets of G k-steps: the next set's LDS reads are
-            // issued (unconditionally) before the current set's fmas
+            // issued (unconditionally) before the current set's fmas (a
+            // scheduling barrier keeps the compiler from sinking them below)
             float xa0[G], xb0[G], xa1[G], xb1[G];
             auto rd = [&](float *xa, float *xb, int kk) {
 #pragma unroll
@@ -214,8 +253,10 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
             rd(xa0, xb0, 0);
             for (int kk = 0; kk < KC; kk += 2 * G) {
                 rd(xa1, xb1, kk + G);
+                __builtin_amdgcn_sched_barrier(0);
                 fm(xa0, xb0);
                 rd(xa0, xb0, kk + 2 * G);  // at the chunk's end: read, not used
+                __builtin_amdgcn_sched_barrier(0);
                 fm(xa1, xb1);
             }
         } else {
@@ -226,6 +267,13 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     }
     const int64_t r = r0 + tr, c = c0 + tc;
     if (r < m && c < n) out[r * n + c] = acc;
+}
+
+// Every byte offset the chain kernel forms (including the past-the-row ones
+// above, up to a chunk and a tile beyond each operand) stays below 2^32.
+bool chain_fits(int64_t m, int64_t k, int64_t n) {
+    const int64_t lim = (int64_t)1 << 30;  // floats
+    return (m + 64) * (k + 1024) < lim && (k + 1024) * (n + 128) < lim;
 }
 
 template <int V>
@@ -253,10 +301,10 @@ int launch_matmul_f32(int variant, const float *a, const float *b, float *out, i
     const int64_t gx = cdiv(n, BN), gy = cdiv(m, BM);
     // The chain kernel for few outputs or few tiles with more than a few
     // k-steps, measured (MI355X, us, chain / tiled, C = A.B): 8x1024x1024
-    // 23.5 / 86, 1x4096x16 45 / 335, 16x4096x4096 88 / 342, 64x1024x1024
-    // 24 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
+    // 13.2 / 86, 1x4096x16 22.5 / 335, 16x4096x4096 49 / 342, 64x1024x1024
+    // 13.4 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
     // 356 / 88, 512^3 48 / 45), and at k = 16 its one step (1x16x4096 6.2 / 3.3).
-    if (k > 64 && (m * n <= 65536 || gx * gy < 64)) {
+    if (k > 64 && (m * n <= 65536 || gx * gy < 64) && chain_fits(m, k, n)) {
         switch (variant) {
         case MM_AB: return launch_chain<MM_AB>(a, b, out, m, k, n, s);
         case MM_ABT: return launch_chain<MM_ABT>(a, b, out, m, k, n, s);
