@@ -199,8 +199,8 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
  * per output over k ascending, then one f32 add to the fused product (which
  * is computed in f32); Y is rounded to y_dtype once.  rank 0 adds nothing.
  * workspace: device memory of at least rq_qmatmul_lora_workspace(...) bytes
- * (f32 copies of X when it is fp16, X.A, (X.A).B, and the fused product when
- * Y is fp16).  Uses the context's GEMM workspace as rq_qmatmul does. */
+ * (f32 copies of X when it is fp16, X.A, and the fused product when Y is
+ * fp16).  Uses the context's GEMM workspace as rq_qmatmul does. */
 size_t rq_qmatmul_lora_workspace(int64_t m, int64_t k_in, int64_t n_out, int64_t rank, rq_dtype x_dtype,
                                  rq_dtype y_dtype);
 int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, const float *lora_a,

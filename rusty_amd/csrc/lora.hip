@@ -4,12 +4,13 @@
 // Here W is the quantized [out, in] weight, so the first term is rq_qmatmul's
 // fused dequant product.  The adapter's two products keep the reference's
 // arithmetic: f32 operands, one fma accumulator per output over k ascending
-// (the f32 matmul kernel, matmul_f32.hip), then one f32 add per output --
-// so with W's term exactly zero the result equals the reference's f32 path
-// bit for bit.  Launches: [x widened to f32], t = x . A, l = t . B, the fused
-// product into f32, y = main + l (rounded to y's dtype).  The adapter's work
-// is (m . in + m . out) . rank fmas and m . (rank + 2 out) floats of traffic:
-// small next to the weight for the ranks adapters use (<= 64).
+// (the f32 matmul kernel, matmul_f32.hip, for x . A; the same chain over
+// the rank for (x . A) . B), then one f32 add per output -- so with W's term
+// exactly zero the result equals the reference's f32 path bit for bit.
+// Launches: [x widened to f32], t = x . A, the fused product into f32, then
+// y = main + t . B (rounded to y's dtype) in one pass.  The adapter's work is
+// (m . in + m . out) . rank fmas and m . (rank + out) + rank . out floats of
+// traffic: small next to the weight for the ranks adapters use (<= 64).
 #include <algorithm>
 
 #include "common.hpp"
@@ -24,13 +25,24 @@ __global__ __launch_bounds__(TH) void k_widen_f16(const _Float16 *__restrict__ x
         out[i] = (float)x[i];
 }
 
-// y = main + l; main may alias y when y is f32.
+// y[i][c] = main[i][c] + sum_r t[i][r] B[r][c], the sum one fma chain from
+// zero over r ascending (the f32 matmul's arithmetic for t . B); main may
+// alias y when y is f32.  Thread c of block (x, y) takes column x TH + c of
+// rows y, y + gridDim.y, ...: B's row r is read coalesced, t's row broadcast.
 template <bool F16>
-__global__ __launch_bounds__(TH) void k_lora_add(const float *main, const float *__restrict__ l, void *y, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * TH + threadIdx.x; i < n; i += (int64_t)gridDim.x * TH) {
-        const float v = main[i] + l[i];
-        if constexpr (F16) static_cast<_Float16 *>(y)[i] = (_Float16)v;
-        else static_cast<float *>(y)[i] = v;
+__global__ __launch_bounds__(TH) void k_lora_out(const float *main, const float *__restrict__ t,
+                                                 const float *__restrict__ b, int rank, void *y, int64_t m,
+                                                 int64_t n) {
+    const int64_t c = (int64_t)blockIdx.x * TH + threadIdx.x;
+    if (c >= n) return;
+    for (int64_t i = blockIdx.y; i < m; i += gridDim.y) {
+        const float *tr = t + i * rank;
+        float acc = 0.0f;
+        for (int r = 0; r < rank; ++r) acc = __builtin_fmaf(tr[r], b[(int64_t)r * n + c], acc);
+        const int64_t o = i * n + c;
+        const float v = main[o] + acc;
+        if constexpr (F16) static_cast<_Float16 *>(y)[o] = (_Float16)v;
+        else static_cast<float *>(y)[o] = v;
     }
 }
 
@@ -46,9 +58,8 @@ extern "C" {
 size_t rq_qmatmul_lora_workspace(int64_t m, int64_t k_in, int64_t n_out, int64_t rank, rq_dtype x_dtype,
                                  rq_dtype y_dtype) {
     if (m < 0 || k_in < 0 || n_out < 0 || rank < 0) return 0;
-    const int64_t floats = (x_dtype == RQ_F16 ? m * k_in : 0) + m * rank + m * n_out +
-                           (y_dtype == RQ_F16 ? m * n_out : 0);
-    return (size_t)floats * 4 + 4 * 256;  // + alignment of each part to 256 bytes
+    const int64_t floats = (x_dtype == RQ_F16 ? m * k_in : 0) + m * rank + (y_dtype == RQ_F16 ? m * n_out : 0);
+    return (size_t)floats * 4 + 3 * 256;  // + alignment of each part to 256 bytes
 }
 
 int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, const float *lora_a,
@@ -65,6 +76,7 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
     if (!mul_ok(m, K, &t) || !mul_ok(m, N, &t) || !mul_ok(m, rank, &t) || !mul_ok(rank, N, &t) ||
         !mul_ok(rank, K, &t))
         return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (rank > 0x7fffffff || cdiv(N, TH) > 0x7fffffff) return fail(RQ_ERR_SHAPE, "adapter rank or n_out too large");
     if (m == 0 || N == 0) return RQ_OK;
     if (!y || (K > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
     if (rank > 0 && (!lora_a || !lora_b)) return fail(RQ_ERR_INVALID_ARGUMENT, "null adapter pointer");
@@ -72,7 +84,7 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
     if (!workspace || workspace_bytes < need)
         return fail(RQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
     hipStream_t s = pick(ctx, stream);
-    // carve the workspace: [x f32][t][l][main f32]
+    // carve the workspace: [x f32][t][main f32]
     char *p = static_cast<char *>(workspace);
     auto carve = [&p](int64_t floats) {
         p = reinterpret_cast<char *>((reinterpret_cast<uintptr_t>(p) + 255) & ~uintptr_t(255));
@@ -91,17 +103,17 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
         xf = w32;
     }
     float *tv = carve(m * rank);
-    float *lv = carve(m * N);
     float *mainv = y_dtype == RQ_F16 ? carve(m * N) : static_cast<float *>(y);
-    // t = x . A [m, rank], l = t . B [m, n_out]: one fma chain per output, k ascending
+    // t = x . A [m, rank]: one fma chain per output, k ascending
     if ((st = launch_matmul_f32(MM_AB, xf, lora_a, tv, m, K, rank, s)) != RQ_OK) return st;
-    if ((st = launch_matmul_f32(MM_AB, tv, lora_b, lv, m, rank, N, s)) != RQ_OK) return st;
     // the fused dequant product, f32
     if ((st = qmatmul_dispatch(ctx, *w, x, x_dtype, mainv, RQ_F32, m, s)) != RQ_OK) return st;
+    // y = main + t . B [m, n_out]
+    const dim3 grid((unsigned)cdiv(N, TH), (unsigned)std::min<int64_t>(m, 65535));
     if (y_dtype == RQ_F16)
-        hipLaunchKernelGGL(k_lora_add<true>, dim3(grid_for(m * N)), dim3(TH), 0, s, mainv, lv, y, m * N);
+        hipLaunchKernelGGL(k_lora_out<true>, grid, dim3(TH), 0, s, mainv, tv, lora_b, (int)rank, y, m, N);
     else
-        hipLaunchKernelGGL(k_lora_add<false>, dim3(grid_for(m * N)), dim3(TH), 0, s, mainv, lv, y, m * N);
+        hipLaunchKernelGGL(k_lora_out<false>, grid, dim3(TH), 0, s, mainv, tv, lora_b, (int)rank, y, m, N);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
