@@ -63,6 +63,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace rq {
 namespace {
@@ -78,57 +79,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // Split-K workspace layout: partial sums per (tile, split) slot of BM x BN f32;
 // one arrival counter per tile on its own 128-byte line.
 constexpr int kSkCounterStride = 32;
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
-}
-
-// A resource whose base and size are wave-uniform values the compiler might
-// still hold in VGPRs (the DMA's inline asm takes its resource in SGPRs):
-// both are passed through readfirstlane first.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_s(const void *p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-    return make_rsrc(reinterpret_cast<const void *>((hi << 32) | lo),
-                     (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
-}
-
-// DMA of 16 bytes per lane: LDS[lds_addr + 16 * lane] = buffer[voff], with
-// lds_addr a 32-bit LDS address (uniform across the wave).  Issued
-// as inline asm so the compiler does not turn its conservative LDS-DMA alias
-// tracking into a full vmcnt(0) wait before every LDS read; every reader of a
-// stage waits with an explicit s_waitcnt vmcnt instead.  M0 carries the LDS
-// base (one wait state before the load, as the ISA requires).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
-    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(l), "v"(voff), "s"(r)
-                 : "memory", "m0");
-}
-
-// DMA of 4 bytes per lane: LDS[lds_addr + 4 * lane] = buffer[voff] (the
-// affine weight's scales of a k-step, see the kernel).
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
-    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                 :
-                 : "s"(l), "v"(voff), "s"(r)
-                 : "memory", "m0");
-}
-
-// Waits until at most N vector-memory operations of this wave are outstanding
-// (they retire in issue order).  Inline asm with a memory clobber, so the
-// compiler cannot move LDS reads of the landed data above the wait.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Waits until every LDS read of this wave has returned its data.
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
 __device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t u, uint32_t sel) {
     const uint32_t m = __builtin_amdgcn_perm(0x64646464u, u, sel);
     const h2_t v = __builtin_bit_cast(h2_t, m) - (h2_t){(_Float16)1152.0f, (_Float16)1152.0f};

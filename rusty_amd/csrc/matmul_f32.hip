@@ -13,6 +13,7 @@
 // Out-of-range rows/columns/k load as zero, which leaves every in-range
 // accumulator unchanged.
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace rq {
 namespace {
@@ -139,9 +140,6 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
 // had just issued, so every chunk paid a memory round trip (1 x 4096 x 16:
 // 45 us).  The host keeps every offset below 2^32 (chain_fits).  Waves whose
 // rows all lie past m skip the chains (m = 1 with 16 rows per block: 3 of 4).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
-}
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
@@ -269,11 +267,183 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     if (r < m && c < n) out[r * n + c] = acc;
 }
 
-// Every byte offset the chain kernel forms (including the past-the-row ones
-// above, up to a chunk and a tile beyond each operand) stays below 2^32.
+// The same chains fed through an LDS ring of NS chunks of KC = 256 k-steps
+// filled by global -> LDS DMA (16 bytes per lane, no registers held), so
+// NS - 1 chunks are in flight while one is multiplied.  A chain advances one
+// dependent fma per 8.4 cycles (MI355X, one wave), 0.9 us per chunk, while a
+// chunk's loads take about two: with one chunk in flight (the register-
+// staged kernel above) every chunk waited for its data.  Each operand keeps
+// its stored layout in LDS, as the DMA writes lane pieces contiguously:
+//  * rows along k (A of MM_AB and MM_ABT, B of MM_ABT): [R][KC + 4], each
+//    row's chunk one 1 KiB DMA unit; the chain reads four k-steps per ds_read_b128;
+//  * rows along the outputs (A of MM_ATB, B of MM_AB and MM_ATB): [KC][C],
+//    C = TR or TC columns, a unit covering 256 / C k-rows; the chain reads
+//    one k-step per element (paired into ds_read2_b32).
+// Units of a chunk: TR for A, TC for B, wave w issuing units w, w + 4, ...
+// Positions past an operand read as zero or land in rows, columns or k that
+// no stored output uses (as above); the dummy DMAs of chunks past K use an
+// offset beyond every resource (operands < 2 GiB, chain_fits).  Requires
+// 16-byte aligned operands and row pitches (ring_ok).
+constexpr int RKC = 256;
+constexpr uint32_t kOOBf = 0x80000000u;  // past every operand resource (operands < 2 GiB)
+template <int V, int TC>
+struct RingShape {
+    static constexpr int TR = TH / TC;
+    static constexpr bool AK = V != MM_ATB;  // A stored with rows along k
+    static constexpr bool BK = V == MM_ABT;  // B stored with rows along k
+    static constexpr int SA = AK ? TR * (RKC + 4) : RKC * TR;  // floats per stage
+    static constexpr int SB = BK ? TC * (RKC + 4) : RKC * TC;
+    static constexpr int ST = SA + SB;
+    static constexpr int NS = 4 * ST * 4 <= 140 * 1024 ? 4 : 3;
+    static constexpr int OPS = (TR + TC) / 4;  // DMA units per wave per chunk
+    static_assert(3 * ST * 4 <= 140 * 1024 && (TR + TC) % 4 == 0, "ring does not fit");
+};
+
+template <int V, int TC>
+__global__ __launch_bounds__(TH) void k_matmul_f32_ring(const float *__restrict__ a, const float *__restrict__ b,
+                                                        float *__restrict__ out, int64_t m, int64_t k, int64_t n) {
+    using RS = RingShape<V, TC>;
+    constexpr int TR = RS::TR, NS = RS::NS, OPS = RS::OPS, SA = RS::SA, ST = RS::ST, AS = RKC + 4;
+    constexpr int G = 32;
+    // (+ G: the chains' reads one register set past a chunk stay inside the ring)
+    __shared__ __attribute__((aligned(1024))) float ring[NS * ST + G * (TR + TC)];
+    const int t = threadIdx.x, lane = t % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(t / 64);
+    const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
+    const int tr = t / TC, tc = t % TC;
+    const uint32_t K = (uint32_t)k, M = (uint32_t)m, N = (uint32_t)n;
+    const auto rsa = make_rsrc(a, (uint32_t)(m * k * 4)), rsb = make_rsrc(b, (uint32_t)(k * n * 4));
+    const uint32_t ring0 = lds_addr(&ring[0]);
+    const int nck = (int)((k + RKC - 1) / RKC);
+
+    // Byte offset of this lane's piece of unit i of chunk c (see above):
+    // rows along k: row i of the panel, k = c KC + 4 lane; rows along the
+    // outputs: k-row c KC + i (256 / C) + lane / (C / 4), columns 4 (lane % (C / 4)).
+    auto off_k = [&](uint32_t row0, uint32_t ld, int i, int c) {
+        return (((row0 + (uint32_t)i) * ld + (uint32_t)(c * RKC)) + 4u * (uint32_t)lane) * 4u;
+    };
+    auto off_o = [&](uint32_t col0, uint32_t ld, int C, int i, int c) {
+        const uint32_t kr = (uint32_t)(c * RKC + i * (256 / C) + lane / (C / 4));
+        return (kr * ld + col0 + 4u * (uint32_t)(lane % (C / 4))) * 4u;
+    };
+    auto issue = [&](int c) {
+        const int s = c % NS;
+        const bool live = c < nck;
+#pragma unroll
+        for (int q = 0; q < OPS; ++q) {
+            const int u = wave + 4 * q;  // wave-uniform
+            if (u < TR) {
+                const uint32_t dst = ring0 + (uint32_t)(s * ST) * 4u + (RS::AK ? (uint32_t)(u * AS) * 4u : (uint32_t)u * 1024u);
+                const uint32_t off = RS::AK ? off_k((uint32_t)r0, K, u, c) : off_o((uint32_t)r0, M, TR, u, c);
+                dma16(rsa, dst, live ? off : kOOBf);
+            } else {
+                const int i = u - TR;
+                const uint32_t dst = ring0 + (uint32_t)(s * ST + SA) * 4u + (RS::BK ? (uint32_t)(i * AS) * 4u : (uint32_t)i * 1024u);
+                const uint32_t off = RS::BK ? off_k((uint32_t)c0, K, i, c) : off_o((uint32_t)c0, N, TC, i, c);
+                dma16(rsb, dst, live ? off : kOOBf);
+            }
+        }
+    };
+
+    const bool idle = r0 + 64 * wave / TC >= m;  // every row of this wave lies past m
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+    for (int c = 0; c < nck; ++c) {
+        wait_vmcnt<(NS - 2) * OPS>();  // this wave's units of chunk c have landed
+        __syncthreads();               // ... and every wave's; chunk c - 1 is no longer read
+        issue(c + NS - 1);             // into chunk c - 1's stage
+        if (idle) continue;
+        const float *sa = ring + (c % NS) * ST, *sb = sa + SA;
+        auto a_at = [&](int kk) -> const float * { return RS::AK ? sa + tr * AS + kk : sa + kk * TR + tr; };
+        auto b_at = [&](int kk) -> const float * { return RS::BK ? sb + tc * AS + kk : sb + kk * TC + tc; };
+        const int64_t k0 = (int64_t)c * RKC;
+        if (k0 + RKC <= k) {
+            float xa0[G], xb0[G], xa1[G], xb1[G];
+            auto rd = [&](float *xa, float *xb, int kk) {
+#pragma unroll
+                for (int i = 0; i < G; i += 4) {
+                    if constexpr (RS::AK) {
+                        const float4 v = *reinterpret_cast<const float4 *>(a_at(kk + i));
+                        xa[i] = v.x;
+                        xa[i + 1] = v.y;
+                        xa[i + 2] = v.z;
+                        xa[i + 3] = v.w;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xa[i + j] = *a_at(kk + i + j);
+                    }
+                    if constexpr (RS::BK) {
+                        const float4 u = *reinterpret_cast<const float4 *>(b_at(kk + i));
+                        xb[i] = u.x;
+                        xb[i + 1] = u.y;
+                        xb[i + 2] = u.z;
+                        xb[i + 3] = u.w;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xb[i + j] = *b_at(kk + i + j);
+                    }
+                }
+            };
+            auto fm = [&](const float *xa, const float *xb) {
+#pragma unroll
+                for (int i = 0; i < G; ++i) acc = __builtin_fmaf(xa[i], xb[i], acc);
+            };
+            rd(xa0, xb0, 0);
+            for (int kk = 0; kk < RKC; kk += 2 * G) {
+                rd(xa1, xb1, kk + G);
+                __builtin_amdgcn_sched_barrier(0);
+                fm(xa0, xb0);
+                rd(xa0, xb0, kk + 2 * G);  // at the chunk's end: read, not used
+                __builtin_amdgcn_sched_barrier(0);
+                fm(xa1, xb1);
+            }
+        } else {
+            const int kc = (int)(k - k0);
+            for (int kk = 0; kk < kc; ++kk) acc = __builtin_fmaf(*a_at(kk), *b_at(kk), acc);
+        }
+    }
+    wait_vmcnt<0>();  // no DMA in flight past this point
+    const int64_t r = r0 + tr, c = c0 + tc;
+    if (r < m && c < n) out[r * n + c] = acc;
+}
+
+// Every byte offset the chain kernels form (including the past-the-row ones
+// above, up to a chunk and a tile beyond each operand) stays below 2^31.
 bool chain_fits(int64_t m, int64_t k, int64_t n) {
-    const int64_t lim = (int64_t)1 << 30;  // floats
+    const int64_t lim = (int64_t)1 << 29;  // floats
     return (m + 64) * (k + 1024) < lim && (k + 1024) * (n + 128) < lim;
+}
+
+// The ring kernel's 16-byte DMA pieces: aligned operands, and every row
+// along which pieces are taken a multiple of 4 floats long.  At n <= 16 with
+// B stored along the outputs (one LDS read per k-step and element) the four
+// waves' reads outweigh the latency the ring hides, and the register-staged
+// kernel stays (MI355X, us, ring / register-staged: 512x4096x16 34.3 / 27.7;
+// 8x1024x1024 9.7 / 13.2, 1x4096x4096 26.0 / 45.6, 16x4096x4096 35.5 / 49;
+// C = A.B^T 512x4096x16 25.8 / 27.0).
+bool ring_ok(int v, const float *a, const float *b, int64_t m, int64_t k, int64_t n) {
+    if (!aligned(a, 16) || !aligned(b, 16)) return false;
+    if (v != MM_ABT && n <= 16) return false;
+    if (v == MM_ATB) return m % 4 == 0 && n % 4 == 0;
+    if (v == MM_ABT) return k % 4 == 0;
+    return k % 4 == 0 && n % 4 == 0;
+}
+
+template <int V>
+int launch_ring(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n, hipStream_t s) {
+    const int tc = n > 16 ? 32 : (n > 8 ? 16 : 8);
+    const int64_t gx = cdiv(n, tc), gy = cdiv(m, TH / tc);
+    if (gx > 0x7fffffff || gy > 65535)
+        return fail(RQ_ERR_SHAPE, "matmul grid too large (m=%lld n=%lld)", (long long)m, (long long)n);
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    switch (tc) {
+    case 32: hipLaunchKernelGGL((k_matmul_f32_ring<V, 32>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 16: hipLaunchKernelGGL((k_matmul_f32_ring<V, 16>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    default: hipLaunchKernelGGL((k_matmul_f32_ring<V, 8>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    }
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
 }
 
 template <int V>
@@ -299,12 +469,20 @@ int launch_matmul_f32(int variant, const float *a, const float *b, float *out, i
                       hipStream_t s) {
     if (m == 0 || n == 0) return RQ_OK;
     const int64_t gx = cdiv(n, BN), gy = cdiv(m, BM);
-    // The chain kernel for few outputs or few tiles with more than a few
+    // The chain kernels for few outputs or few tiles with more than a few
     // k-steps, measured (MI355X, us, chain / tiled, C = A.B): 8x1024x1024
-    // 13.2 / 86, 1x4096x16 22.5 / 335, 16x4096x4096 49 / 342, 64x1024x1024
-    // 13.4 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
+    // 9.7 / 86, 1x4096x16 22.5 / 335, 16x4096x4096 35.5 / 342, 64x1024x1024
+    // 9.9 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
     // 356 / 88, 512^3 48 / 45), and at k = 16 its one step (1x16x4096 6.2 / 3.3).
     if (k > 64 && (m * n <= 65536 || gx * gy < 64) && chain_fits(m, k, n)) {
+        if (ring_ok(variant, a, b, m, k, n)) {
+            switch (variant) {
+            case MM_AB: return launch_ring<MM_AB>(a, b, out, m, k, n, s);
+            case MM_ABT: return launch_ring<MM_ABT>(a, b, out, m, k, n, s);
+            case MM_ATB: return launch_ring<MM_ATB>(a, b, out, m, k, n, s);
+            default: break;
+            }
+        }
         switch (variant) {
         case MM_AB: return launch_chain<MM_AB>(a, b, out, m, k, n, s);
         case MM_ABT: return launch_chain<MM_ABT>(a, b, out, m, k, n, s);
