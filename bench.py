@@ -383,18 +383,26 @@ def ops_bench(ctx, engine, use_graph: bool = True) -> list:
     after >= 0.25 s of warm-up replays, median of 3) against its roofline:
       dequantize          a2, kernels.wgsl:153-166: 1 B read + 4 B written per element
       affine_dequantize   a1, kernels.wgsl:379-400: + 8 B (scale, bias) per 64 elements
-      matmul_f32          a3, kernels.wgsl:7-54: 2 m k n flops, fp32 VALU
+      matmul_f32          a3, kernels.wgsl:7-54: 2 m k n flops, fp32 VALU; at configs[0]'s few
+                          outputs the bound is the k-long dependent fma chain of each output,
+                          reported as the one-launch time of one wave's chain of k fmas
       qmatmul_dx          f-4, MatMulNode::backward: dX = dY . deq(W), 2 m n k flops, fp32 VALU
       qmatmul_lora        a7 with an adapter, lib.rs:69-83: the fused product plus (x.A).B
     The dequantize kernels rotate 8 inputs and 4 outputs (384 MB, past the
     256 MB Infinity Cache)."""
-    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, synth
+    from rusty_amd import DType, QuantizedTensor, UnifiedTensor, _lib, synth
 
     g = synth.rng(5)
     out = []
 
     def timed(fn, calls):
         return sorted(t / calls * 1e3 for t in _replays(ctx, fn, calls, use_graph))[1]  # us per call
+
+    probe_out = UnifiedTensor.empty(ctx, [64], DType.FP32)
+
+    def chain_floor(steps):  # us: one launch of one wave's `steps` dependent fmas
+        return timed(lambda: [_lib.call("rq_fma_chain_probe", ctx.handle, steps, probe_out.ptr, None)
+                              for _ in range(4)], 4)
 
     n = 4096 * 4096
     words = [UnifiedTensor.new(ctx, g.integers(0, 256, n, dtype=np.uint8), dtype=DType.U8) for _ in range(8)]
@@ -423,6 +431,8 @@ def ops_bench(ctx, engine, use_graph: bool = True) -> list:
              "gflops": round(gf, 1), "frac_fp32_peak": round(gf / 1e3 / FP32_PEAK_TFLOPS, 4)}
         if (m, k, nn) == (4096, 4096, 4096):
             e["vs_published_m2"] = round(gf / REF_MATMUL_4096_GFLOPS, 1)
+        else:
+            e["chain_floor_us"] = round(chain_floor(k), 2)
         out.append(e)
         del a, b, c
 
@@ -447,6 +457,7 @@ def ops_bench(ctx, engine, use_graph: bool = True) -> list:
         base = timed(lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(4)], 4)
         out.append({"op": "qmatmul_lora", "ref": "rusty-graph/src/lib.rs:69-83", "m": m, "n_out": 4096, "k_in": 4096,
                     "rank": rank, "us": round(us, 2), "us_without_adapter": round(base, 2),
+                    "adapter_chain_floor_us": round(chain_floor(4096), 2),
                     "what": "y fp16 = x . deq(W)^T + (x . A) . B; the same weight every call (L2/MALL-resident)"})
     return out
 

@@ -104,6 +104,12 @@ int rq_device_clock(rq_ctx *ctx, uint64_t *dst, uint64_t *ticks_per_second, rq_s
  * read (and read + store) floor for the same bytes. */
 int rq_stream_probe(rq_ctx *ctx, const void *src, size_t row_bytes, size_t rows, int rows_per_block, void *dst,
                     int store, rq_stream stream);
+/* A measurement aid with no counterpart in the reference: one wave of 64
+ * lanes runs `steps` dependent f32 fmas (acc = fma(acc, a, b)) and stores the
+ * 64 results to dst (64 floats).  Timed beside the f32 matmul it gives the
+ * one-launch floor of a k-ascending fma chain of the same length (the bound
+ * of that kernel where few outputs each walk a long k). */
+int rq_fma_chain_probe(rq_ctx *ctx, int64_t steps, float *dst, rq_stream stream);
 /* Human-readable name of a status code, and the calling thread's last error
  * message (empty string if none). */
 const char *rq_status_string(int status);

@@ -90,6 +90,7 @@ _SIGNATURES = {
     "rq_sync": [_P, _P],
     "rq_device_delay": [_P, c_uint32, _P],
     "rq_stream_probe": [_P, _P, c_size_t, c_size_t, c_int, _P, c_int, _P],
+    "rq_fma_chain_probe": [_P, ctypes.c_int64, _P, _P],
     "rq_device_clock": [_P, _P, POINTER(ctypes.c_uint64), _P],
     "rq_status_string": [c_int],
     "rq_last_error": [],

@@ -125,6 +125,21 @@ void launch_probe(int cpt, unsigned blocks, hipStream_t s, const uint8_t *src, i
     }
 }
 
+// One wave, `steps` dependent f32 fmas per lane (acc = fma(acc, a, b), a and
+// b kernel arguments so nothing folds), the result stored: the latency of a
+// k-ascending fma chain, which bounds the f32 matmul's chain kernels where
+// few outputs each walk a long k.
+__global__ __launch_bounds__(64) void k_fma_chain_probe(float a, float b, int64_t steps, float *__restrict__ dst) {
+    float acc = (float)threadIdx.x;
+    int64_t i = 0;
+    for (; i + 16 <= steps; i += 16) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(acc, a, b);
+    }
+    for (; i < steps; ++i) acc = __builtin_fmaf(acc, a, b);
+    dst[threadIdx.x] = acc;
+}
+
 // Byte fill: 16-byte stores over the aligned middle (grid-stride), single
 // bytes for the unaligned head and tail.  A kernel rather than
 // hipMemsetAsync, so that a caller may capture it in a HIP graph: memset
@@ -267,6 +282,15 @@ int rq_device_clock(rq_ctx *ctx, uint64_t *dst, uint64_t *ticks_per_second, rq_s
         *ticks_per_second = (uint64_t)khz * 1000u;
     }
     hipLaunchKernelGGL(k_device_clock, dim3(1), dim3(64), 0, pick(ctx, stream), dst);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+int rq_fma_chain_probe(rq_ctx *ctx, int64_t steps, float *dst, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (!dst) return fail(RQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (steps < 0) return fail(RQ_ERR_SHAPE, "negative step count");
+    hipLaunchKernelGGL(k_fma_chain_probe, dim3(1), dim3(64), 0, pick(ctx, stream), 1.0000001f, 1e-7f, steps, dst);
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }

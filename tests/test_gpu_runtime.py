@@ -1,7 +1,8 @@
 """Measurement aids and memory plumbing of the C ABI: rq_device_delay (the
 bounded device-side wait that benchmark drivers put in front of a batch of
-direct launches) and rq_stream_probe (the GEMV's weight stream alone), neither
-with a reference counterpart, and rq_memset."""
+direct launches), rq_stream_probe (the GEMV's weight stream alone) and
+rq_fma_chain_probe (one wave's dependent fma chain), none with a reference
+counterpart, and rq_memset."""
 import pytest
 
 from rusty_amd import _lib
@@ -167,6 +168,38 @@ def test_stream_probe_limits(ctx):
     assert lib.rq_stream_probe(ctx.handle, 16, 24, 1, 1, 16, 1, None) == _lib.RQ_ERR_SHAPE
     assert lib.rq_stream_probe(ctx.handle, 16, 16, 1, 5, 16, 1, None) == _lib.RQ_ERR_SHAPE
     assert lib.rq_stream_probe(ctx.handle, 16, 16384 + 16, 1, 1, 16, 1, None) == _lib.RQ_ERR_SHAPE
+
+
+# rq_fma_chain_probe: lane l of one wave runs acc = fma(acc, a, b) from acc = l,
+# a = 1.0000001f, b = 1e-7f; checked against the C library's fmaf (one rounding).
+
+@pytest.mark.parametrize("steps", [0, 1, 37, 1000])
+def test_fma_chain_probe(ctx, steps):
+    import ctypes
+
+    import numpy as np
+
+    from rusty_amd import DType, UnifiedTensor
+
+    libm = ctypes.CDLL("libm.so.6")
+    libm.fmaf.restype = ctypes.c_float
+    libm.fmaf.argtypes = [ctypes.c_float] * 3
+    a, b = float(np.float32(1.0000001)), float(np.float32(1e-7))
+    want = np.zeros(64, np.float32)
+    for lane in range(64):
+        acc = float(lane)
+        for _ in range(steps):
+            acc = libm.fmaf(acc, a, b)
+        want[lane] = acc
+    d = UnifiedTensor.new(ctx, np.full(64, np.nan, np.float32))
+    _lib.call("rq_fma_chain_probe", ctx.handle, steps, d.ptr, None)
+    np.testing.assert_array_equal(d.to_vec(), want)
+
+
+def test_fma_chain_probe_limits(ctx):
+    lib = _lib.lib()
+    assert lib.rq_fma_chain_probe(ctx.handle, 10, None, None) == _lib.RQ_ERR_INVALID_ARGUMENT
+    assert lib.rq_fma_chain_probe(ctx.handle, -1, 16, None) == _lib.RQ_ERR_SHAPE
 
 
 # rq_device_clock: device wall-clock stamps on the stream (graph-capturable)
