@@ -45,6 +45,24 @@ def test_adapter_term_bit_exact(ctx, engine, m, xdt):
     np.testing.assert_array_equal(Y.to_vec().reshape(m, n), want)
 
 
+# ranks past the kernels' register-held paths (16, 64): the generic loop
+@pytest.mark.parametrize("m,rank", [(3, 70), (300, 5)])
+def test_adapter_term_bit_exact_ranks(ctx, engine, m, rank):
+    g = synth.rng(m + rank)
+    n, k = 192, 256
+    u = g.integers(0, 256, size=(n, k), dtype=np.uint8)
+    zeros = np.zeros(n * k // 64, np.float32)
+    W = QuantizedTensor.affine(ctx, u, zeros, zeros)  # deq(W) = 0 exactly
+    x = synth.activations(g, m, k, dtype=np.float32)
+    a, b = _adapter(g, k, n, rank)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP32)
+    A, B = UnifiedTensor.new(ctx, a), UnifiedTensor.new(ctx, b)
+    Y = UnifiedTensor.new(ctx, np.full((m, n), np.nan, np.float32))
+    engine.qmatmul_lora(ctx, X, W, A, B, Y)
+    want = orc.matmul(orc.matmul(x, a, fused=True), b, fused=True)
+    np.testing.assert_array_equal(Y.to_vec().reshape(m, n), want)
+
+
 @pytest.mark.parametrize("m,fmt,ydt", [(1, 0, np.float16), (4, 1, np.float32), (16, 0, np.float32),
                                        (64, 1, np.float16), (512, 0, np.float16)])
 def test_full_output_against_truth(ctx, engine, m, fmt, ydt):
