@@ -67,6 +67,9 @@ int launch_rowwise_dequantize(const int8_t *q, const float *scales, float *out, 
                               int64_t k, hipStream_t s);
 int launch_matmul_f32(int variant, const float *a, const float *b, float *out, int64_t m, int64_t k,
                       int64_t n, hipStream_t s);
+// C = A.B with fp16 A where the chain kernel takes it directly; RQ_ERR_UNSUPPORTED otherwise.
+int launch_matmul_f32_ah(const _Float16 *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
+                         hipStream_t s);
 int launch_gemv_decode(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int m, hipStream_t s);
 // m = 1..4 decode GEMV that adds its result into an f32 y (y += X . deq(W)^T):
 // the residual connection fused into the projection's epilogue.

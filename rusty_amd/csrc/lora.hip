@@ -7,7 +7,8 @@
 // (the f32 matmul kernel, matmul_f32.hip, for x . A; the same chain over
 // the rank for (x . A) . B), then one f32 add per output -- so with W's term
 // exactly zero the result equals the reference's f32 path bit for bit.
-// Launches: [x widened to f32], t = x . A, the fused product into f32, then
+// Launches: [x widened to f32, where the chain kernel does not take fp16 x
+// itself], t = x . A, the fused product into f32, then
 // y = main + t . B (rounded to y's dtype) in one pass.  The adapter's work is
 // (m . in + m . out) . rank fmas and m . (rank + out) + rank . out floats of
 // traffic: small next to the weight for the ranks adapters use (<= 64).
@@ -112,20 +113,27 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
         p += floats * 4;
         return r;
     };
-    const float *xf = static_cast<const float *>(x);
-    if (x_dtype == RQ_F16) {
-        float *w32 = carve(m * K);
-        if (m * K > 0) {
-            hipLaunchKernelGGL(k_widen_f16, dim3(grid_for(m * K)), dim3(TH), 0, s, static_cast<const _Float16 *>(x),
-                               w32, m * K);
-            RQ_LAUNCH_CHECK();
-        }
-        xf = w32;
-    }
+    float *w32 = x_dtype == RQ_F16 ? carve(m * K) : nullptr;
     float *tv = carve(m * rank);
     float *mainv = y_dtype == RQ_F16 ? carve(m * N) : static_cast<float *>(y);
-    // t = x . A [m, rank]: one fma chain per output, k ascending
-    if ((st = launch_matmul_f32(MM_AB, xf, lora_a, tv, m, K, rank, s)) != RQ_OK) return st;
+    // t = x . A [m, rank]: one fma chain per output, k ascending.  fp16 x:
+    // the chain kernel widens it while staging where it serves the shape,
+    // else x is widened to f32 first (exact either way).
+    st = x_dtype == RQ_F16 ? launch_matmul_f32_ah(static_cast<const _Float16 *>(x), lora_a, tv, m, K, rank, s)
+                           : RQ_ERR_UNSUPPORTED;
+    if (st == RQ_ERR_UNSUPPORTED) {
+        const float *xf = static_cast<const float *>(x);
+        if (x_dtype == RQ_F16) {
+            if (m * K > 0) {
+                hipLaunchKernelGGL(k_widen_f16, dim3(grid_for(m * K)), dim3(TH), 0, s,
+                                   static_cast<const _Float16 *>(x), w32, m * K);
+                RQ_LAUNCH_CHECK();
+            }
+            xf = w32;
+        }
+        st = launch_matmul_f32(MM_AB, xf, lora_a, tv, m, K, rank, s);
+    }
+    if (st != RQ_OK) return st;
     // the fused dequant product, f32
     if ((st = qmatmul_dispatch(ctx, *w, x, x_dtype, mainv, RQ_F32, m, s)) != RQ_OK) return st;
     // y = main + t . B [m, n_out]: enough row groups for ~4 blocks per CU,

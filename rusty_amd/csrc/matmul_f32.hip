@@ -147,9 +147,14 @@ __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 template <int TC>
 constexpr int chain_kc() { return TC == 16 || TC == 32 ? 512 : 256; }  // 64-80 KiB of LDS per chunk
 
-template <int V, int TC>
-__global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict__ a, const float *__restrict__ b,
+// AH: A holds fp16 values (MM_AB only), loaded as 2-byte elements and
+// widened exactly when staged -- the f32 matmul of the widened copy, without
+// the copy (a LoRA adapter's x . A on fp16 activations).
+template <int V, int TC, bool AH = false>
+__global__ __launch_bounds__(TH) void k_matmul_f32_chain(const void *__restrict__ a, const float *__restrict__ b,
                                                          float *__restrict__ out, int64_t m, int64_t k, int64_t n) {
+    static_assert(!AH || V == MM_AB, "fp16 A: C = A.B only");
+    constexpr uint32_t EA = AH ? 2u : 4u;  // bytes per A element
     constexpr int TR = TH / TC;
     constexpr int KC = chain_kc<TC>();
     constexpr int P = KC / TH;                       // chunk rows of TH elements per contiguous row piece
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
     const int tr = t / TC, tc = t % TC;  // this thread's output
     const uint32_t K = (uint32_t)k, M = (uint32_t)m, N = (uint32_t)n;
-    const auto ra_ = make_rsrc(a, (uint32_t)(m * k * 4)), rb_ = make_rsrc(b, (uint32_t)(k * n * 4));
+    const auto ra_ = make_rsrc(a, (uint32_t)(m * k * EA)), rb_ = make_rsrc(b, (uint32_t)(k * n * 4));
     // Element e of this thread in a chunk: LDS index and byte offset from the
     // thread's base offset (uniform per e); the bases advance by a chunk.
     //  A [m, k] (A [k, m] for MM_ATB), B [k, n] (B [n, k] for MM_ABT).
@@ -173,8 +178,8 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
         va = ((uint32_t)(t / TR) * M + (uint32_t)r0 + (uint32_t)(t % TR)) * 4u;
         da = (uint32_t)KC * M * 4u;
     } else {
-        va = ((uint32_t)r0 * K + (uint32_t)t) * 4u;
-        da = (uint32_t)KC * 4u;
+        va = ((uint32_t)r0 * K + (uint32_t)t) * EA;
+        da = (uint32_t)KC * EA;
     }
     if constexpr (V == MM_ABT) {
         vb = ((uint32_t)c0 * K + (uint32_t)t) * 4u;
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     }
     auto a_soff = [&](int e) -> uint32_t {
         if constexpr (V == MM_ATB) return (uint32_t)(TC * e) * M * 4u;
-        else return (uint32_t)(e / P) * K * 4u + (uint32_t)(e % P) * (TH * 4u);
+        else return (uint32_t)(e / P) * K * EA + (uint32_t)(e % P) * (TH * EA);
     };
     auto a_lds = [&](int e) {
         if constexpr (V == MM_ATB) return (t % TR) * AS + t / TR + TC * e;
@@ -199,10 +204,15 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
         if constexpr (V == MM_ABT) return (e / P) * AS + t + TH * (e % P);
         else return (t % TC) * AS + t / TC + TR * e;
     };
-    float ra[NA], rb[NB];
+    float ra[NA], rb[NB];  // AH: ra holds the raw fp16 bits
     auto load = [&]() {
 #pragma unroll
-        for (int e = 0; e < NA; ++e) ra[e] = bload(ra_, va, a_soff(e));
+        for (int e = 0; e < NA; ++e) {
+            if constexpr (AH)
+                ra[e] = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ra_, va, a_soff(e), 0));
+            else
+                ra[e] = bload(ra_, va, a_soff(e));
+        }
 #pragma unroll
         for (int e = 0; e < NB; ++e) rb[e] = bload(rb_, vb, b_soff(e));
         va += da;
@@ -210,7 +220,12 @@ __global__ __launch_bounds__(TH) void k_matmul_f32_chain(const float *__restrict
     };
     auto stage = [&]() {
 #pragma unroll
-        for (int e = 0; e < NA; ++e) As[a_lds(e)] = ra[e];
+        for (int e = 0; e < NA; ++e) {
+            if constexpr (AH)
+                As[a_lds(e)] = (float)__builtin_bit_cast(_Float16, (uint16_t)__builtin_bit_cast(uint32_t, ra[e]));
+            else
+                As[a_lds(e)] = ra[e];
+        }
 #pragma unroll
         for (int e = 0; e < NB; ++e) Bs[b_lds(e)] = rb[e];
     };
@@ -446,18 +461,18 @@ int launch_ring(const float *a, const float *b, float *out, int64_t m, int64_t k
     return RQ_OK;
 }
 
-template <int V>
-int launch_chain(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n, hipStream_t s) {
+template <int V, bool AH = false>
+int launch_chain(const void *a, const float *b, float *out, int64_t m, int64_t k, int64_t n, hipStream_t s) {
     const int tc = n >= 64 ? 64 : (n > 16 ? 32 : (n > 8 ? 16 : 8));
     const int64_t gx = cdiv(n, tc), gy = cdiv(m, TH / tc);
     if (gx > 0x7fffffff || gy > 65535)
         return fail(RQ_ERR_SHAPE, "matmul grid too large (m=%lld n=%lld)", (long long)m, (long long)n);
     const dim3 grid((unsigned)gx, (unsigned)gy);
     switch (tc) {
-    case 64: hipLaunchKernelGGL((k_matmul_f32_chain<V, 64>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
-    case 32: hipLaunchKernelGGL((k_matmul_f32_chain<V, 32>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
-    case 16: hipLaunchKernelGGL((k_matmul_f32_chain<V, 16>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
-    default: hipLaunchKernelGGL((k_matmul_f32_chain<V, 8>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 64: hipLaunchKernelGGL((k_matmul_f32_chain<V, 64, AH>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 32: hipLaunchKernelGGL((k_matmul_f32_chain<V, 32, AH>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    case 16: hipLaunchKernelGGL((k_matmul_f32_chain<V, 16, AH>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
+    default: hipLaunchKernelGGL((k_matmul_f32_chain<V, 8, AH>), grid, dim3(TH), 0, s, a, b, out, m, k, n); break;
     }
     RQ_LAUNCH_CHECK();
     return RQ_OK;
@@ -502,6 +517,17 @@ int launch_matmul_f32(int variant, const float *a, const float *b, float *out, i
     }
     RQ_LAUNCH_CHECK();
     return RQ_OK;
+}
+
+// C = A.B with A fp16 (exactly widened), where the register-staged chain
+// kernel serves the shape (few outputs, n <= 16, k > 64); RQ_ERR_UNSUPPORTED
+// (nothing launched) otherwise, and the caller widens A itself.
+int launch_matmul_f32_ah(const _Float16 *a, const float *b, float *out, int64_t m, int64_t k, int64_t n,
+                         hipStream_t s) {
+    if (m == 0 || n == 0) return RQ_OK;
+    const int64_t gx = cdiv(n, BN), gy = cdiv(m, BM);
+    if (!(k > 64 && (m * n <= 65536 || gx * gy < 64) && chain_fits(m, k, n)) || n > 16) return RQ_ERR_UNSUPPORTED;
+    return launch_chain<MM_AB, true>(a, b, out, m, k, n, s);
 }
 
 }  // namespace rq

@@ -45,21 +45,24 @@ def test_adapter_term_bit_exact(ctx, engine, m, xdt):
     np.testing.assert_array_equal(Y.to_vec().reshape(m, n), want)
 
 
-# ranks past the kernels' register-held paths (16, 64): the generic loop
-@pytest.mark.parametrize("m,rank", [(3, 70), (300, 5)])
-def test_adapter_term_bit_exact_ranks(ctx, engine, m, rank):
+# other ranks: past the output kernel's register-held B columns (70), and
+# fp16 x at rank <= 16, where x . A's chain kernel widens x while staging
+# instead of through an f32 copy
+@pytest.mark.parametrize("m,rank,xdt", [(3, 70, np.float32), (300, 5, np.float32), (1, 16, np.float16),
+                                        (2, 9, np.float16), (300, 16, np.float16)])
+def test_adapter_term_bit_exact_ranks(ctx, engine, m, rank, xdt):
     g = synth.rng(m + rank)
     n, k = 192, 256
     u = g.integers(0, 256, size=(n, k), dtype=np.uint8)
     zeros = np.zeros(n * k // 64, np.float32)
     W = QuantizedTensor.affine(ctx, u, zeros, zeros)  # deq(W) = 0 exactly
-    x = synth.activations(g, m, k, dtype=np.float32)
+    x = synth.activations(g, m, k, dtype=xdt)
     a, b = _adapter(g, k, n, rank)
-    X = UnifiedTensor.new(ctx, x, dtype=DType.FP32)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16 if xdt == np.float16 else DType.FP32)
     A, B = UnifiedTensor.new(ctx, a), UnifiedTensor.new(ctx, b)
     Y = UnifiedTensor.new(ctx, np.full((m, n), np.nan, np.float32))
     engine.qmatmul_lora(ctx, X, W, A, B, Y)
-    want = orc.matmul(orc.matmul(x, a, fused=True), b, fused=True)
+    want = orc.matmul(orc.matmul(x.astype(np.float32), a, fused=True), b, fused=True)
     np.testing.assert_array_equal(Y.to_vec().reshape(m, n), want)
 
 
