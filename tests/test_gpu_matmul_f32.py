@@ -22,7 +22,10 @@ pytestmark = pytest.mark.gpu
 # oracle bit for bit.
 SHAPES = [(2, 2, 2), (1, 1024, 1024), (8, 1024, 1024), (65, 33, 70), (128, 256, 96), (3, 0, 5), (1, 4096, 4096),
           (1, 4097, 16), (5, 1000, 40), (33, 600, 9), (7, 300, 3), (2, 513, 100), (512, 4096, 16),
-          (512, 200, 520), (1030, 64, 600)]
+          (512, 200, 520), (1030, 64, 600),
+          # the DMA-ring chain kernel (16-byte rows, n > 16 or A.B^T): ragged row and
+          # column blocks with a partial last chunk, for all three variants
+          (20, 520, 44), (12, 700, 36)]
 
 
 def _run(engine, ctx, op, a, b, m, n):
