@@ -519,6 +519,7 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
         if ((st = launch_rope_scatter(md->pqkv, md->rope, p0, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
                                       md->pq, kc, vc, s)))
             return st;
+        if (l == c.n_layers - 1) break;  // the last layer's rest: below, for the last position only
         if ((st = launch_attn_prefill(md->pq, kc, vc, md->patt, p0, n, c.n_heads, c.n_kv_heads, c.head_dim,
                                       c.max_seq, s)))
             return st;
@@ -527,7 +528,29 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
         if ((st = swiglu_run(md->ctx, L.gate, L.up, L.down, md->pxn, RQ_F16, md->ph, md->py, RQ_F32, n, ws, s)))
             return st;
     }
+    // Past its KV-cache write, the last layer matters only through the last
+    // position's output, and only in the final chunk (a later chunk starts
+    // again from embeddings): its attention runs for the last query tile, its
+    // o projection, norm and MLP for the last row (the decode GEMVs).
     if (!end) return RQ_OK;
+    {
+        const rq_llama::Layer &L = md->layers[c.n_layers - 1];
+        const size_t l = (size_t)c.n_layers - 1, qrow = (size_t)c.n_heads * c.head_dim;
+        const int t0 = 32 * ((n - 1) / 32);  // first row of the last query tile
+        if ((st = launch_attn_prefill(md->pq + t0 * qrow, md->kc + l * kv_layer, md->vc + l * kv_layer,
+                                      md->patt + t0 * qrow, p0 + t0, n - t0, c.n_heads, c.n_kv_heads, c.head_dim,
+                                      c.max_seq, s)))
+            return st;
+        const size_t last = (size_t)(n - 1);
+        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt + last * qrow, RQ_F16, md->py + last * H, RQ_F32, 1, s)))
+            return st;
+        if ((st = launch_add_rmsnorm_rows(md->px + last * H, md->py + last * H, L.mlp_norm, c.norm_eps,
+                                          md->pxn + last * H, 1, H, s)))
+            return st;
+        if ((st = swiglu_run(md->ctx, L.gate, L.up, L.down, md->pxn + last * H, RQ_F16, md->ph, md->py + last * H,
+                             RQ_F32, 1, ws, s)))
+            return st;
+    }
     // the last position only: x += down projection, logits, greedy pick
     float *xl = md->px + (size_t)(n - 1) * H;
     if ((st = launch_add_rmsnorm_rows(xl, md->py + (size_t)(n - 1) * H, nullptr, 0.0f, nullptr, 1, H, s))) return st;
