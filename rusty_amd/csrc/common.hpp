@@ -100,6 +100,17 @@ struct GemmWorkspace {
 // The workspace of ctx when work on stream s may use it: the context's own
 // stream only (two GEMMs running at once on different streams would share it).
 GemmWorkspace gemm_workspace(const rq_ctx *ctx, hipStream_t s);
+// The outputs of launch_gemm_qkv_rope (a Llama layer's packed q/k/v projection
+// over positions p0 .. of a prompt chunk): this layer's K and V caches
+// [n_kv][max_seq][64] fp16 and the rotation table rope[pos * 32 + d] =
+// (cos, sin) of position pos and pair d; q goes to the call's q argument.
+struct RopeOut {
+    const float2 *rope = nullptr;
+    _Float16 *kc = nullptr, *vc = nullptr;
+    int p0 = 0, n_heads = 0, n_kv = 0, max_seq = 0;
+};
+int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, const RopeOut &ro, _Float16 *q,
+                         int num_cus, const GemmWorkspace &ws, hipStream_t s);
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s);
 // h = fp16(silu(X . deq(gate)^T) * (X . deq(up)^T)) in one GEMM launch, g and

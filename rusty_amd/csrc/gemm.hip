@@ -145,14 +145,20 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
 // (g and u rounded to fp16 first, as a separate silu*mul pass over stored
 // g and u would see them) to Yv, fp16 [M][I] (I % 8 == 0).  Only the two
 // large tiles are built with it (the smaller ones run near the SGPR limit).
+// ROPE (BN = 64 = head_dim, per-row codes, no split): the tile's 64 features
+// are one head of the packed q/k/v output, and the epilogue applies the
+// rotary embedding to q and k heads -- o[d] = a c - b s, o[d + 32] = a s + b c
+// for a, b the f32 results at d and d + 32 -- and writes q (Yv) and the K and
+// V caches (RopeOut) in fp16 instead of the f32 product.
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, int FMT = 0,
-          bool PAIR = false>
+          bool PAIR = false, bool ROPE = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                      const _Float16 *__restrict__ X, void *__restrict__ Yv,
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm, int splits, float *__restrict__ skw,
                                                      int *__restrict__ skc, int group, const uint8_t *__restrict__ Wb,
-                                                     const float *__restrict__ scalesb, int n_split) {
+                                                     const float *__restrict__ scalesb, int n_split, RopeOut ro) {
+    static_assert(!ROPE || (BN == 64 && FMT == 0 && !PAIR), "rotary epilogue: one 64-wide head per tile");
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -300,6 +306,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     esc[io][g][r] = scl[wr < NL ? wr : 0];
                 }
             }
+    }
+    // ROPE: the (cos, sin) of the pairs 4 (t % 8) .. + 3 at the positions of
+    // the tile rows this thread writes (32 ps + t / 8), requested here for the
+    // same reason (also for a v head, which does not use them: no branch)
+    constexpr int RRP = NW * 64 / 8;  // epilogue rows per pass: 8 threads per row
+    float4 rcs[ROPE ? BM / RRP : 1][2];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int ps = 0; ps < BM / RRP; ++ps) {
+            const int sr = min(m0 + ps * RRP + t / 8, M - 1);
+            const float4 *rp = reinterpret_cast<const float4 *>(ro.rope + (size_t)(ro.p0 + sr) * 32 + 4 * (t % 8));
+            rcs[ps][0] = rp[0];
+            rcs[ps][1] = rp[1];
+        }
     }
 
     // A k-step's fragments: raw int8 W (expanded just before the MFMA) and fp16 X.
@@ -658,6 +678,37 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
             }
         }
         __syncthreads();
+        if constexpr (ROPE) {
+            // 8 threads per tile row: thread c rotates the pairs (4c + e, 4c + e + 32)
+            const int c = t % 8, hh = n0 / 64, kvh = hh - ro.n_heads;
+            const bool rot = kvh < ro.n_kv;  // q and k heads; v is copied
+#pragma unroll
+            for (int ps = 0; ps < BM / RRP; ++ps) {
+                const int row = ps * RRP + t / 8, sr = m0 + row;
+                if (sr >= M) continue;
+                const float4 a = *reinterpret_cast<const float4 *>(ot + row * RS + c * 16);
+                const float4 b = *reinterpret_cast<const float4 *>(ot + row * RS + (c + 8) * 16);
+                const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+                const float cs[8] = {rcs[ps][0].x, rcs[ps][0].y, rcs[ps][0].z, rcs[ps][0].w,
+                                     rcs[ps][1].x, rcs[ps][1].y, rcs[ps][1].z, rcs[ps][1].w};
+                h2_t lo[2], hi[2];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float cx = cs[2 * e], sy = cs[2 * e + 1];
+                    lo[e / 2][e % 2] = (_Float16)(rot ? av[e] * cx - bv[e] * sy : av[e]);
+                    hi[e / 2][e % 2] = (_Float16)(rot ? av[e] * sy + bv[e] * cx : bv[e]);
+                }
+                const int pos = ro.p0 + sr;
+                _Float16 *dst = hh < ro.n_heads ? static_cast<_Float16 *>(Yv) + ((size_t)sr * ro.n_heads + hh) * 64
+                                : rot ? ro.kc + ((size_t)kvh * ro.max_seq + pos) * 64
+                                      : ro.vc + ((size_t)(kvh - ro.n_kv) * ro.max_seq + pos) * 64;
+                *reinterpret_cast<uint2 *>(dst + 4 * c) =
+                    make_uint2(__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1]));
+                *reinterpret_cast<uint2 *>(dst + 32 + 4 * c) =
+                    make_uint2(__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1]));
+            }
+            return;
+        }
         constexpr int OB = PAIR ? HB * 2 : BN * EB;  // output bytes per tile row
         constexpr int CPR = OB / 16;                 // 16-byte pieces per tile row
         constexpr int RPP = 64 * NW / CPR;           // rows per pass
@@ -688,7 +739,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ry, off, 0, 2);
         }
     };
-    if constexpr (PAIR) {
+    if constexpr (ROPE) {
+        staged(std::integral_constant<int, 4>{});  // f32 rows, rotated and written as fp16 q / k / v
+        return;
+    } else if constexpr (PAIR) {
         staged(std::integral_constant<int, 2>{});  // the host guarantees I % 8 == 0 and fp16 h
         return;
     } else {
@@ -758,14 +812,15 @@ struct GemmPair {
 
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, bool PAIR = false>
 int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
-                 int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{}) {
+                 int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{},
+                 const RopeOut *rope = nullptr) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     if (tiles > 0x7fffffff) return RQ_ERR_UNSUPPORTED;
     const int64_t nk = K / 64;
     int64_t splits = 1;
-    if (BM == 64 && BN == 64 && ws.partials && nk >= 16 && 4 * tiles <= 3 * cus && tiles <= ws.n_counters) {
+    if (BM == 64 && BN == 64 && !rope && ws.partials && nk >= 16 && 4 * tiles <= 3 * cus && tiles <= ws.n_counters) {
         splits = std::min<int64_t>(nk / 8, 2 * tiles <= cus ? cus / tiles : 2);
         while (splits > 1 && (size_t)(tiles * splits) * BM * BN > ws.floats) --splits;
         splits = cdiv(nk, cdiv(nk, splits));  // every split gets k-steps (the kernel's ks = ceil(nk / splits))
@@ -774,8 +829,15 @@ int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *
         hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * splits)), dim3(64 * NW), 0, s, (const uint8_t *)w.codes,
                            scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m,
                            tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64,
-                           pair.w, pair.scales, (int)(pair.n_split ? pair.n_split : N));
+                           pair.w, pair.scales, (int)(pair.n_split ? pair.n_split : N), rope ? *rope : RopeOut{});
     };
+    if constexpr (BN == 64 && !PAIR) {
+        if (rope) {
+            go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, false, true>);
+            RQ_LAUNCH_CHECK();
+            return RQ_OK;
+        }
+    }
     if constexpr (PAIR) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, true>);
     else if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
     else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0>);
@@ -819,6 +881,13 @@ __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, _
     }
 }
 
+// Whether a grid of bm x bn tiles over m x N still has >= 2/3 as many tiles as
+// the device has CUs (and the tile is not taller than the tokens, rounded up
+// to 64): the tile choice below.
+bool tile_fills(int64_t m, int64_t N, int64_t cus, int bm, int bn) {
+    return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus;
+}
+
 // The fp16-activation GEMM over m rows, tile chosen by shape.
 int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
                int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{}) {
@@ -840,7 +909,7 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
     // it fills the device whenever 256x128 would.
     // a tile taller than the tokens (rounded up to 64) only multiplies padding:
     // 64 x 11008 x 4096 took 23.6 us on 128x64 tiles, 17.7 on split 64x64 ones
-    auto fills = [&](int bm, int bn) { return bm <= std::max<int64_t>(64, m) && cdiv(m, bm) * cdiv(N, bn) * 3 >= 2 * cus; };
+    auto fills = [&](int bm, int bn) { return tile_fills(m, N, cus, bm, bn); };
     if (pair.n_split) {  // gate and up: the two large tiles only (the caller falls back otherwise)
         if (fills(128, 256))
             return launch_tiled<128, 256, true, 4, 8, 4, 2, true, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, pair);
@@ -872,6 +941,27 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
 // leave the block.  Per-row int8 weights of one shape, fp16 activations,
 // I % 8 == 0; RQ_ERR_UNSUPPORTED otherwise, or when the grid is too small for
 // the two large tiles.
+// A Llama layer's packed q/k/v projection with the rotary epilogue (see
+// k_gemm_rowwise, ROPE): q fp16 [m][n_heads][64] to q, k and v into the
+// caches at positions ro.p0 .. ro.p0 + m - 1.  Per-row int8 weights of
+// (n_heads + 2 n_kv) 64 rows, fp16 x, and a token count whose tile choice is
+// 64 wide (64x64 or 128x64); RQ_ERR_UNSUPPORTED (nothing launched) otherwise,
+// and the caller runs the product and the rotation separately.
+int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, const RopeOut &ro, _Float16 *q,
+                         int num_cus, const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t N = w.n_out, K = w.k_in;
+    if (w.format != RQ_Q_ROWWISE_I8 || K % 64 != 0 || K > (1 << 21) || m < 1 || m > 0x7fffffff ||
+        N != (int64_t)(ro.n_heads + 2 * ro.n_kv) * 64 || !ro.rope || !ro.kc || !ro.vc || !aligned(w.codes, 16) ||
+        !aligned(x, 16) || !aligned(q, 8) || !aligned(ro.kc, 8) || !aligned(ro.vc, 8) || !aligned(ro.rope, 16) ||
+        (int64_t)ro.p0 + m > ro.max_seq)
+        return RQ_ERR_UNSUPPORTED;
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    if (tile_fills(m, N, cus, 128, 256) || tile_fills(m, N, cus, 128, 128)) return RQ_ERR_UNSUPPORTED;
+    if (tile_fills(m, N, cus, 128, 64))
+        return launch_tiled<128, 64, true, 6, 4, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+    return launch_tiled<64, 64, true, 4, 4, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+}
+
 int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
                        int num_cus, const GemmWorkspace &ws, hipStream_t s) {
     const int64_t I = gate.n_out, K = gate.k_in;

@@ -514,11 +514,27 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
         // x += (previous layer's down projection), xn = rmsnorm(x)
         if ((st = launch_add_rmsnorm_rows(md->px, l ? md->py : nullptr, L.attn_norm, c.norm_eps, md->pxn, n, H, s)))
             return st;
-        if ((st = qmatmul_dispatch(md->ctx, L.qkv, md->pxn, RQ_F16, md->pqkv, RQ_F32, n, s))) return st;
         _Float16 *kc = md->kc + l * kv_layer, *vc = md->vc + l * kv_layer;
-        if ((st = launch_rope_scatter(md->pqkv, md->rope, p0, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
-                                      md->pq, kc, vc, s)))
+        // q/k/v with the rotation in the GEMM's epilogue where its tiles are one
+        // head wide; else the f32 product, then the rotation and cache writes
+        RopeOut ro;
+        ro.rope = md->rope;
+        ro.kc = kc;
+        ro.vc = vc;
+        ro.p0 = p0;
+        ro.n_heads = c.n_heads;
+        ro.n_kv = c.n_kv_heads;
+        ro.max_seq = c.max_seq;
+        st = c.head_dim == 64 ? launch_gemm_qkv_rope(L.qkv, md->pxn, n, ro, md->pq, md->ctx->num_cus, ws, s)
+                              : RQ_ERR_UNSUPPORTED;
+        if (st == RQ_ERR_UNSUPPORTED) {
+            if ((st = qmatmul_dispatch(md->ctx, L.qkv, md->pxn, RQ_F16, md->pqkv, RQ_F32, n, s))) return st;
+            if ((st = launch_rope_scatter(md->pqkv, md->rope, p0, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
+                                          md->pq, kc, vc, s)))
+                return st;
+        } else if (st != RQ_OK) {
             return st;
+        }
         if (l == c.n_layers - 1) break;  // the last layer's rest: below, for the last position only
         if ((st = launch_attn_prefill(md->pq, kc, vc, md->patt, p0, n, c.n_heads, c.n_kv_heads, c.head_dim,
                                       c.max_seq, s)))
