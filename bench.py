@@ -503,11 +503,20 @@ def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eag
     b.synchronize()
     stepwise_ms = a.elapsed_ms(b)
     runner.close()
-    # prefill work: every Linear over the prompt's rows, causal attention
-    # (q.k and p.v over positions 0..s for every head), one lm_head row
-    lin = sum(n * k for n, k in cfg.linear_shapes().values())
-    pf_flops = (2 * prompt_len * lin * cfg.n_layers + 2 * cfg.vocab * cfg.hidden
-                + cfg.n_layers * 4 * cfg.n_heads * cfg.head_dim * prompt_len * (prompt_len + 1) // 2)
+    # prefill work as performed: every Linear over the prompt's rows and causal
+    # attention (q.k and p.v over positions 0..s for every head) in all but
+    # the last layer; there q/k/v over every row (the KV cache), attention for
+    # the last query tile of 32 positions, the other Linears for the last row;
+    # one lm_head row
+    shapes = cfg.linear_shapes()
+    lin = sum(n * k for n, k in shapes.values())
+    lin_qkv = sum(shapes[nm][0] * shapes[nm][1] for nm in ("q", "k", "v"))
+    t0 = 32 * ((prompt_len - 1) // 32)
+    attn_pos = 4 * cfg.n_heads * cfg.head_dim  # flops per (query, key) pair
+    pf_flops = (2 * prompt_len * lin * (cfg.n_layers - 1) + 2 * prompt_len * lin_qkv + 2 * (lin - lin_qkv)
+                + 2 * cfg.vocab * cfg.hidden
+                + (cfg.n_layers - 1) * attn_pos * prompt_len * (prompt_len + 1) // 2
+                + attn_pos * sum(p + 1 for p in range(t0, prompt_len)))
     kv_row = cfg.n_kv_heads * cfg.head_dim * 2 * 2  # K and V, fp16, one position
     kv = cfg.n_layers * kv_row * sum(prompt_len + i + 1 for i in range(steps)) / steps
     per_tok = cfg.weight_bytes() + kv + cfg.hidden * 2
