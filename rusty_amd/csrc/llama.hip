@@ -153,11 +153,13 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
 // bytes) through one CU, so splitting a head's context over S blocks divides
 // that stream; the first pass's rows are requested right after pos is read,
 // before the RoPE prologue.  A pass covers 8 waves x RW consecutive rows
-// each; lane l holds 16-byte chunk l % CH of row i * RPI + l / CH for i < 4,
+// each; lane l holds 16-byte chunk l % CH of row i * RPI + l / CH for i < NI,
 // all in flight before any is used.  The block's work is a serial chain of
 // short dependent steps, so it is spread thin: 8 waves of 4 row loads
 // measured 1.4-1.6 % more tokens/s for the whole decode step than 4 waves of
-// 8 (16 waves of 2: +0.7 %).  Row scores finish with DPP steps over the CH
+// 8 (16 waves of 2: +0.7 %), and 8 waves of 2 another 1.0 % (an 80-row
+// split then keeps 5 waves busy instead of 3; 8 waves of 1 load, two passes
+// per split: -1.0 %).  Row scores finish with DPP steps over the CH
 // lanes of a row; P.V partials are summed over the lanes of a chunk, then over
 // waves in LDS; passes beyond the first combine by the online-softmax rescale.
 constexpr int ATT = 512;  // threads per attention block
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     constexpr int NW = ATT / 64;
     constexpr int CH = HD / 8;         // 16-byte chunks per row
     constexpr int RPI = 64 / CH;       // rows per wave-wide load
-    constexpr int NI = 4;              // loads of K (and of V) per lane per pass
+    constexpr int NI = 2;              // loads of K (and of V) per lane per pass
     constexpr int RW = NI * RPI;       // rows per wave per pass
     constexpr int PASS = NW * RW;      // positions per pass
     constexpr int HALF = HD / 2;

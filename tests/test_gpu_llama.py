@@ -63,8 +63,8 @@ def run_collect(runner, prompt, steps):
 def test_small_models_match_oracle(ctx, cfg):
     # the runner splits each head's attention over 1 (max_seq <= 160), 2 (<= 320), 4 (<= 480) or 8
     # blocks: these models cover 1 and 2 at head_dim 64, 1 and 4 and 8 at head_dim 128 (the 1.1B test:
-    # 8 at 64); a pass covers 128 rows at head_dim 128 and 256 at 64, and no split here exceeds one
-    # pass -- test_attention_multi_pass covers that
+    # 8 at 64); a pass covers 64 rows at head_dim 128 and 128 at 64: the 600-position model's
+    # splits (75 rows) take two passes, test_attention_multi_pass covers longer ones
     w = synth_weights(cfg, seed=cfg.hidden + cfg.vocab)
     g = np.random.default_rng(11)
     n_prompt = min(40, cfg.max_seq // 2) if cfg.max_seq < 200 else 280
@@ -201,9 +201,10 @@ def test_llama_1b_128_greedy_steps(ctx):
 ], ids=["hd128_1100", "hd64_2200"])
 def test_attention_multi_pass(ctx, cfg, n_prompt):
     """Caches long enough that each of the 8 splits per head spans more than one
-    pass of the attention kernel (128 rows at head_dim 128: 129-138 rows per
-    split here; 256 rows at head_dim 64: 258-275): the later passes' loads, the
-    online-softmax rescale and the pass-end barriers, against the f64 oracle."""
+    pass of the attention kernel (64 rows at head_dim 128: 129-138 rows per
+    split here, three passes; 128 rows at head_dim 64: 258-275, three passes):
+    the later passes' loads, the online-softmax rescale and the pass-end
+    barriers, against the f64 oracle."""
     w = synth_weights(cfg, seed=cfg.max_seq)
     prompt = np.random.default_rng(cfg.max_seq).integers(0, cfg.vocab, n_prompt)
     steps = cfg.max_seq - n_prompt
