@@ -96,17 +96,25 @@ __global__ __launch_bounds__(TH) void k_matmul_f32(const float *__restrict__ a, 
         }
         __syncthreads();
         if (k0 + BK < k) load(k0 + BK);
+        // the LDS values of step kk + 2 are requested before step kk's fmas
+        // (three register sets, the loop fully unrolled)
+        float av[3][4], bv[3][4];
+        auto rd = [&](int st, int kk) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[st][i] = As[kk][ty + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[st][j] = Bs[kk][tx + 16 * j];
+        };
+        rd(0, 0);
+        rd(1, 1);
 #pragma unroll
         for (int kk = 0; kk < BK; ++kk) {
-            float av[4], bv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) av[i] = As[kk][ty + 16 * i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx + 16 * j];
+            if (kk + 2 < BK) rd((kk + 2) % 3, kk + 2);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[kk % 3][i], bv[kk % 3][j], acc[i][j]);
         }
         __syncthreads();
     }
