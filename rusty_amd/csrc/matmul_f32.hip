@@ -496,7 +496,7 @@ int launch_matmul_f32(int variant, const float *a, const float *b, float *out, i
     // k-steps, measured (MI355X, us, chain / tiled, C = A.B): 8x1024x1024
     // 9.7 / 86, 1x4096x16 22.5 / 335, 16x4096x4096 35.5 / 342, 64x1024x1024
     // 9.9 / 86; with more outputs the tiled kernel's reuse wins (256x1024x4096
-    // 356 / 88, 512^3 48 / 45), and at k = 16 its one step (1x16x4096 6.2 / 3.3).
+    // 356 / 74, 512^3 48 / 38), and at k = 16 its one step (1x16x4096 6.2 / 3.3).
     if (k > 64 && (m * n <= 65536 || gx * gy < 64) && chain_fits(m, k, n)) {
         if (ring_ok(variant, a, b, m, k, n)) {
             switch (variant) {
