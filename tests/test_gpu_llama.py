@@ -229,13 +229,29 @@ def _tie_model():
     return w, q, s
 
 
-def _pick(ctx, w, n_prompt=5):
+def _pick(ctx, w, n_prompt=5, steps=3):
+    """The prompt's pick (end of the batched prefill), then `steps` decode
+    steps through the step graph: (token, logits) of the prompt, and of each
+    step."""
     r = LlamaRunner(ctx, TINY, w)
     r.prefill(np.arange(1, n_prompt + 1))
     logits = r.logits()
     tok = int(r.tokens()[n_prompt])
+    dec = []
+    for i in range(steps):
+        r.decode(1)
+        dec.append((int(r.tokens()[n_prompt + 1 + i]), r.logits()))
     r.close()
-    return tok, logits
+    return tok, logits, dec
+
+
+def _check_steps_pick(dec, ties):
+    # every decode step's token is the reference pick of that step's logits; with
+    # `ties`, the step's largest logit is held by several rows (exactly equal)
+    for i, (tok, lg) in enumerate(dec):
+        assert tok == ol.greedy(lg.astype(np.float64)), (i, tok)
+        if ties:
+            assert np.count_nonzero(lg == lg.max()) >= 2, (i, lg.max())
 
 
 def test_greedy_pick_ties_and_threshold(ctx):
@@ -245,7 +261,7 @@ def test_greedy_pick_ties_and_threshold(ctx):
     w, q, s = _tie_model()
     q[0, 0], s[0] = 127, 1.0
     w.lm_head = (q, s)
-    _, lg = _pick(ctx, w)
+    _, lg, _ = _pick(ctx, w, steps=0)
     sgn = 1.0 if lg[0] > 0 else -1.0
     assert lg[0] != 0.0
 
@@ -257,10 +273,13 @@ def test_greedy_pick_ties_and_threshold(ctx):
     for r_ in (200, 900):
         q[r_, 0], s[r_] = int(-127 * sgn), 1e6
     w.lm_head = (q, s)
-    tok, lg = _pick(ctx, w)
+    tok, lg, dec = _pick(ctx, w)
     assert lg[300] > 0 and lg[300] == lg[640] == lg[941], (lg[300], lg[640], lg[941])
     assert tok == 300, tok
     assert tok == ol.greedy(lg.astype(np.float64))
+    # the decode steps: 300 again where xn0 keeps its sign, else 200 (first of 200, 900)
+    _check_steps_pick(dec, ties=True)
+    assert all(t in (200, 300) for t, _ in dec), [t for t, _ in dec]
 
     # nothing above -1e9: every logit is very negative, rows >= 100 less so than
     # rows < 100 (the largest is at 100), but all are <= -1e9, so the pick is 0
@@ -269,7 +288,8 @@ def test_greedy_pick_ties_and_threshold(ctx):
     s[:] = 1e12
     s[:100] = 2e12
     w.lm_head = (q, s)
-    tok, lg = _pick(ctx, w)
+    tok, lg, dec = _pick(ctx, w)
     assert lg.max() <= -1e9 and lg.argmax() == 100, (lg.max(), lg.argmax())
     assert tok == 0, tok
     assert tok == ol.greedy(lg.astype(np.float64))
+    _check_steps_pick(dec, ties=False)
