@@ -134,7 +134,9 @@ __device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 
 // each split into two fp16 terms multiplied separately; per-row codes enter
 // as exact fp16 values, affine codes as exact u with the group's scale and
 // bias applied in f32 after the MFMAs (u . x and the group sum of x).
-template <bool SWI, int NWV, int FMT = 0, bool XF = false>
+// XFIRST: each batch's activation loads are issued before its weight loads
+// (see launch_mfma).
+template <bool SWI, int NWV, int FMT = 0, bool XF = false, bool XFIRST = false>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                   const int8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                   const void *__restrict__ X, void *__restrict__ Yv, int y_f16,
@@ -218,23 +220,34 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             const float *bp = up ? biases2 : biases;
             b.b[0] = bp ? __builtin_bit_cast(float4, bload<0>(make_rsrc(bp, bytes), off)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        auto wloads = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the weight block
-            const bool live = klive && r < rows_here;
-            const uint32_t off = (uint32_t)r * (uint32_t)K + k0 + 16u * (uint32_t)fr;
-            b.w[i] = bload<2>(SWI && i >= 2 ? rw2 : rw, live ? off : kOOB);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t k = k0 + 32u * (uint32_t)j;  // lane k = k + 8 q .. + 8
-            const bool live = k + 8u * (uint32_t)q < (uint32_t)K;
-            if constexpr (XF) {
-                b.x[2 * j] = bload<0>(rx, live ? xbase + k * 4u : kOOB);
-                b.x[2 * j + 1] = bload<0>(rx, live ? xbase + k * 4u + 16u : kOOB);
-            } else {
-                b.x[j] = bload<0>(rx, live ? xbase + k * 2u : kOOB);
+            for (int i = 0; i < 4; ++i) {
+                const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the weight block
+                const bool live = klive && r < rows_here;
+                const uint32_t off = (uint32_t)r * (uint32_t)K + k0 + 16u * (uint32_t)fr;
+                b.w[i] = bload<2>(SWI && i >= 2 ? rw2 : rw, live ? off : kOOB);
             }
+        };
+        auto xloads = [&]() {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t k = k0 + 32u * (uint32_t)j;  // lane k = k + 8 q .. + 8
+                const bool live = k + 8u * (uint32_t)q < (uint32_t)K;
+                if constexpr (XF) {
+                    b.x[2 * j] = bload<0>(rx, live ? xbase + k * 4u : kOOB);
+                    b.x[2 * j + 1] = bload<0>(rx, live ? xbase + k * 4u + 16u : kOOB);
+                } else {
+                    b.x[j] = bload<0>(rx, live ? xbase + k * 2u : kOOB);
+                }
+            }
+        };
+        if constexpr (XFIRST) {
+            xloads();
+            wloads();
+        } else {
+            wloads();
+            xloads();
         }
     };
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -406,10 +419,17 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
             hipLaunchKernelGGL((k_gemv_mfma<true, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
                                (const int8_t *)w.codes, w.scales, (const int8_t *)w2->codes, w2->scales, x, y, 1, m,
                                (int)N, (int)K, w.biases, w2->biases);
-        else
-            hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
-                               (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
-                               (int)N, (int)K, w.biases, nullptr);
+        else {
+            constexpr bool XFP = NW == 8 && F == 0 && !XF;  // the activation-first variant exists
+            if (XFP && m >= 8)
+                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF, XFP>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+                                   (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
+                                   (int)N, (int)K, w.biases, nullptr);
+            else
+                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+                                   (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
+                                   (int)N, (int)K, w.biases, nullptr);
+        }
     };
     auto go_fmt = [&](auto nwv, auto xfc) {
         if (affine) go(nwv, std::integral_constant<int, 1>{}, xfc);
@@ -419,6 +439,12 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
         if (xf) go_fmt(nwv, std::true_type{});
         else go_fmt(nwv, std::false_type{});
     };
+    // Activations before weights in each batch (XFIRST) for per-row codes and
+    // fp16 x at 8 waves and m >= 8, where the block's activation block (m x K
+    // fp16, re-read by every block) is the longest-waiting load: 4096^2 m = 8 /
+    // 12 / 16 6.03 -> 5.90, 6.68 -> 6.43, 7.34 -> 7.0 us.  Slower at m = 4
+    // (5.70 -> 5.81), at 4 waves (11008 x 4096 m = 16 16.5 -> 17.1) and for
+    // affine codes (m = 16 7.9 -> 8.4).
     // affine codes with f32 activations hold four scale and bias vectors per
     // batch: at 8 waves (256 VGPRs each) they spill, at 4 they fit
     const bool wide = K <= 4096 && blocks <= 512 && !(affine && xf);
