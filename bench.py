@@ -16,7 +16,9 @@ Printed JSON (one line, stdout):
   floor            the same weight bytes read without the GEMV's arithmetic
                    (and with its output store): the one-launch floor
   cpu_baseline     the reference's per-token path on host cores: k-ascending
-                   f32 GEMV on the load-time-dequantized f32 weight (oracle port)
+                   f32 GEMV on the load-time-dequantized f32 weight (oracle port);
+                   `legs`: the same path at configs[0] and at the configs[3]
+                   prefill shape (a bounded sample of its tokens)
   prefill          dequant-GEMM TFLOPS at M=2048 for the three configs[3] shapes
   prefill_mid      the same GEMM at M=256 and 512 (4096x4096), not a configs[] shape
   decode_gemv      GB/s at M=1/4/16 and the SwiGLU shapes (configs[1], [2]), the
@@ -28,7 +30,8 @@ Printed JSON (one line, stdout):
   decode_tok_s     configs[4]: 1.1B int8 Llama, 512-token prompt, then 128
                    greedy decode steps timed (HIP events), tokens/s; `decode`
                    also holds the batched prefill of that prompt (tokens/s,
-                   TFLOPS of its GEMM + attention work) next to the stepwise one
+                   TFLOPS of its GEMM + attention work) next to the stepwise one;
+                   `decode_affine` the same on the reference's affine u8 weights
   ops              the path's other operations, each against its roofline: the
                    reference's two dequantize kernels (4096^2 elements), its f32
                    tiled matmul (k-ascending, bit-exact with the reference's order;
@@ -468,16 +471,19 @@ def _lora_workspace(m, k, n, rank):
     return int(_lib.lib().rq_qmatmul_lora_workspace(m, k, n, rank, 1, 1))
 
 
-def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False) -> dict:
+def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False,
+                affine_group: int = 0) -> dict:
     """1.1B int8 Llama greedy decode, one HIP-graph launch per token.
     Algorithmic bytes per token = int8 codes + f32 scales of every Linear and
     the lm_head + the fp16 KV cache rows attention reads (positions 0..pos,
-    once per KV head) + one fp16 embedding row."""
+    once per KV head) + one fp16 embedding row.  With ``affine_group`` every
+    Linear is in the reference's affine u8 format (f32 scale and bias per
+    group), whose scale and bias bytes count instead."""
     from rusty_amd.hiprt import Event
     from rusty_amd.llama import LLAMA_1B, LlamaRunner, synth_weights
 
     cfg = LLAMA_1B
-    runner = LlamaRunner(ctx, cfg, synth_weights(cfg, seed=0))
+    runner = LlamaRunner(ctx, cfg, synth_weights(cfg, seed=0, affine_group=affine_group))
     if eager:
         runner.set_graph(False)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, prompt_len)
@@ -519,13 +525,15 @@ def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eag
                 + attn_pos * sum(p + 1 for p in range(t0, prompt_len)))
     kv_row = cfg.n_kv_heads * cfg.head_dim * 2 * 2  # K and V, fp16, one position
     kv = cfg.n_layers * kv_row * sum(prompt_len + i + 1 for i in range(steps)) / steps
-    per_tok = cfg.weight_bytes() + kv + cfg.hidden * 2
+    per_tok = cfg.weight_bytes(affine_group) + kv + cfg.hidden * 2
     tok_s = steps / (best * 1e-3)
     gbs = per_tok * tok_s / 1e9
     return {"tok_s": round(tok_s, 1), "ms_per_token": round(best / steps, 4), "bytes_per_token": int(per_tok),
             "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "config": "1.1B: 22 layers, hidden 2048, 32/4 heads x 64, SwiGLU 5632, vocab 32000; "
                       f"{prompt_len}-token random prompt, {steps} greedy steps timed, best of {reps}",
+            "weights": (f"affine u8, f32 scale + bias per {affine_group} (the reference's format)" if affine_group
+                        else "per-row int8, f32 scale per row"),
             "generated_head": [int(t) for t in toks[prompt_len:prompt_len + 8]],
             "prefill": {"tok_s": round(prompt_len / (best_pf * 1e-3), 1), "ms": round(best_pf, 3),
                         "tflops": round(pf_flops / (best_pf * 1e-3) / 1e12, 1),
@@ -573,7 +581,60 @@ def cpu_baseline(seconds: float):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port",
             "sample": (f"{steps} per-token steps of the reference path (k-ascending f32 fma GEMV on the "
                        f"load-time-dequantized f32 weight, configs[1] shape 4096x4096 M=1) in {el:.1f} s; "
-                       f"bytes counted as the int8 algorithmic bytes of the GPU step")}
+                       f"bytes counted as the int8 algorithmic bytes of the GPU step"),
+            "legs": [cpu_leg_config0(seconds / 2), cpu_leg_config3(seconds / 2)]}
+
+
+def _timed_forward(ref, x, y, seconds):
+    _, threads = ref.forward(x, y)  # warm
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        ref.forward(x, y)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return steps, el, threads
+
+
+def cpu_leg_config0(seconds: float) -> dict:
+    """configs[0] on host cores: the reference's Linear (load-time f32
+    dequantization, then matmul_tiled's k-ascending f32 sum) at X f32 [8, 1024]
+    . W [1024, 1024], GFLOPS of 2 M N K per step."""
+    from oracle import oracle as orc
+    from rusty_amd import synth
+
+    g = synth.rng(0)
+    q, s = synth.rowwise_weight(g, 1024, 1024)
+    x = synth.activations(g, 8, 1024, dtype=np.float32)
+    ref = orc.RefLinear(q, s, None, 0)
+    y = np.empty((8, 1024), np.float32)
+    steps, el, threads = _timed_forward(ref, x, y, seconds)
+    gf = 2 * 8 * 1024 * 1024 * steps / el / 1e9
+    return {"config": "configs[0]", "value": round(gf, 3), "unit": "GFLOPS", "cores": int(threads), "kind": "port",
+            "sample": f"{steps} steps of Y f32 [8,1024] = X . deq(W)^T, W int8 [1024,1024] per-row scale, "
+                      f"in {el:.1f} s (the whole configs[0] workload per step)"}
+
+
+def cpu_leg_config3(seconds: float, rows: int = 64) -> dict:
+    """configs[3] on host cores: the same reference path at the prefill shape
+    (W [4096, 4096]), timed on a bounded sample of the 2048 tokens (``rows``
+    of them per step: each output is one k-ascending chain, so the rate per
+    token does not depend on how many tokens a step holds); TFLOPS of 2 rows
+    N K per step."""
+    from oracle import oracle as orc
+    from rusty_amd import synth
+
+    g = synth.rng(0)
+    q, s = synth.rowwise_weight(g, 4096, 4096)
+    x = synth.activations(g, rows, 4096, sigma=0.5, dtype=np.float32)
+    ref = orc.RefLinear(q, s, None, 0)
+    y = np.empty((rows, 4096), np.float32)
+    steps, el, threads = _timed_forward(ref, x, y, seconds)
+    tf = 2 * rows * 4096 * 4096 * steps / el / 1e12
+    return {"config": "configs[3]", "value": round(tf, 5), "unit": "TFLOPS", "cores": int(threads), "kind": "port",
+            "sample": f"{steps} steps of {rows} of the 2048 prefill tokens, X f32 [{rows},4096] . deq(W)^T, "
+                      f"W int8 [4096,4096] per-row scale, in {el:.1f} s; the full 2048-token step would take "
+                      f"{2048 / rows * el / steps:.1f} s"}
 
 
 def vendor_gemm(reps: int = 5) -> list:
@@ -693,6 +754,7 @@ def main() -> int:
             out["ops"] = ops_bench(ctx, engine, use_graph=not args.no_graph)
         else:
             out["decode"] = decode_loop(ctx, eager=args.decode_eager)
+            out["decode_affine"] = decode_loop(ctx, eager=args.decode_eager, affine_group=64)
         log(f"{out}")
         ctx.close()
         print(json.dumps(out), flush=True)
@@ -761,6 +823,9 @@ def main() -> int:
         result["decode_tok_s"] = dec["tok_s"]
         result["prefill_tok_s"] = dec["prefill"]["tok_s"]
         result["decode"] = dec
+        # configs[4] on the reference's own weight format (affine u8, group 64)
+        result["decode_affine"] = decode_loop(ctx, affine_group=64)
+        log(f"decode (affine weights) {result['decode_affine']}")
         result["ops"] = ops_bench(ctx, engine)
         for e in result["ops"]:
             log(f"op {e}")

@@ -60,6 +60,8 @@ typedef struct rq_qweight {
     int64_t k_in;
     int32_t format;       /* rq_qformat                                    */
     int32_t group;        /* AFFINE: elements per group (64 in reference)  */
+    const float *prep;    /* AFFINE, optional: the table rq_qweight_prepare
+                           * built from these scales and biases, or NULL   */
 } rq_qweight;
 
 typedef struct rq_ctx rq_ctx;
@@ -157,6 +159,24 @@ int rq_affine_dequantize(rq_ctx *ctx, const uint32_t *weight, size_t n_weight_wo
  * shape, lib.rs:172-174,206). */
 int rq_qweight_dequantize(rq_ctx *ctx, const rq_qweight *w, float *out, rq_stream stream);
 
+/* Load-time preparation of an affine weight for the prefill GEMM: the step
+ * WeightsContext::upload_quantized (rusty-loader/src/lib.rs:155-218) runs
+ * once per weight at load (there, dequantization to f32).  The GEMM reads an
+ * affine weight's scales per k-step and row as a table
+ * table[g][0][n] = s[n][g], table[g][1][n] = b[n][g] - 1024 s[n][g]
+ * (g < k_in / group, the bias term folded with the fp16 expansion's offset).
+ * rq_qweight_prep_bytes gives its size in bytes: 8 * n_out * k_in / group
+ * for an affine weight whose group is a multiple of 64 dividing k_in (what
+ * the GEMM serves), else 0 (nothing to prepare).  rq_qweight_prepare builds
+ * the table into `table` (device, 16-byte aligned, table_bytes >= that size)
+ * on `stream` and sets w->prep = table; with a size of 0 it only sets
+ * w->prep = NULL.  A weight without a table still works: every GEMM call
+ * then builds it again in the context's preparation area (context stream
+ * only).  The table depends on the scale and bias values: rebuild it if they
+ * change.  No reference counterpart as an entry point. */
+size_t rq_qweight_prep_bytes(const rq_qweight *w);
+int rq_qweight_prepare(rq_ctx *ctx, rq_qweight *w, void *table, size_t table_bytes, rq_stream stream);
+
 /* ---- f32 matmul family (the reference's per-token GEMMs) ---------------
  * All row-major f32, one f32 sum per output in ascending k, each step a fused
  * multiply-add.  m, k, n as the host derives them from tensor shapes. */
@@ -183,11 +203,14 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * Tensor::matmul, rusty-autograd/src/lib.rs:468-477).
  * x_dtype/y_dtype: RQ_F16 or RQ_F32; accumulation is f32.
  * m <= 16 runs the decode GEMV kernels, larger m the MFMA GEMM.  f32
- * activations keep f32 accuracy up to m = 16 (each value carried as two fp16
- * terms, the weights as exact code values) for values in fp16's range
- * (|x| <= 65504; below 6.1e-5 a value keeps fp16-subnormal precision, which
- * matters only if a whole row is that small); the GEMM rounds them to fp16
- * (the fp16-MFMA prefill path), as it does affine weights.  On the
+ * activations keep f32 accuracy up to m = 16: each value is carried as two
+ * fp16 terms (the weights as exact code values) after an exact power-of-two
+ * scaling -- per 16-value chunk of a row for m <= 2; for 3..16 rows, per
+ * 256-k batch whenever a value passes fp16's range (65504) -- so any finite
+ * f32 row is served (at 3..16 rows a row whose values all lie below 6.1e-5
+ * keeps fp16-subnormal precision); the GEMM rounds them to fp16 (the
+ * fp16-MFMA prefill path; values past 65504 become infinite there), as it
+ * does affine weights.  On the
  * context's own stream (stream NULL) a GEMM with few tokens splits K over
  * more blocks using the context's workspace, so two such calls of one
  * context must not run concurrently (they cannot on one stream); on any
@@ -226,10 +249,14 @@ int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, con
 
 /* No counterpart in the reference: rq_mlp_swiglu for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that
- * forbid hipMalloc).  Same kernels and results as rq_mlp_swiglu, but the
- * intermediate h lives in a library-owned device array of 8 MiB per device
- * (held until the process ends) instead of a caller workspace, so the call
- * allocates nothing; the prefill GEMMs of this variant do not split K.
+ * forbid hipMalloc).  Same kernels as rq_mlp_swiglu, but the intermediate h
+ * lives in a library-owned device array of 8 MiB per device (held until the
+ * process ends) instead of a caller workspace, so the call allocates nothing,
+ * and none of its GEMMs (gate/up or down) uses the context's workspace: they
+ * never split K (so a prefill result may differ from rq_mlp_swiglu's in the
+ * summation order where that one splits), and f32 activations or affine
+ * weights without a prepared table (rq_qweight_prepare) at m > 16 take the
+ * generic kernel.
  * Limit: 4 * m * intermediate <= 8 MiB (m * intermediate <= 2,097,152), else
  * RQ_ERR_SHAPE.  All calls on one device share that device's array: calls
  * that overlap on one device (other streams, other threads) race and must be
@@ -296,8 +323,10 @@ typedef struct rq_llama_weights {
 
 typedef struct rq_llama rq_llama;
 
-/* Validates the weights against the config, packs q/k/v, allocates the KV
- * cache and step state, and captures the step graph on the context stream. */
+/* Validates the weights against the config, packs q/k/v and allocates the KV
+ * cache and step state.  The step graph is captured later, by the first step
+ * that runs in graph mode (see rq_llama_decode), so a runner that only steps
+ * eagerly never captures one. */
 int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weights *w, rq_llama **out);
 int rq_llama_destroy(rq_llama *model);
 /* Starts a sequence: runs the n prompt tokens (host array, each < vocab)
@@ -316,7 +345,9 @@ int rq_llama_prefill(rq_llama *model, const int32_t *tokens, int32_t n, rq_strea
 int rq_llama_set_prefill(rq_llama *model, int32_t rows);
 /* n_steps greedy decode steps, each feeding the previous token.  The
  * sequence grows by n_steps; fails with RQ_ERR_SHAPE past max_seq cached
- * positions.  Asynchronous (graph launches only). */
+ * positions.  Asynchronous (graph launches only).  In graph mode the first
+ * step of the runner's life captures and instantiates the step graph on
+ * `stream` (stream capture, no device work) before launching it. */
 int rq_llama_decode(rq_llama *model, int32_t n_steps, rq_stream stream);
 /* Steps run as one graph launch each (default, use_graph = 1) or as direct
  * kernel launches on the stream (0: for tools that do not trace graphs). */

@@ -39,6 +39,7 @@ class rq_qweight(ctypes.Structure):
         ("k_in", c_int64),
         ("format", c_int32),
         ("group", c_int32),
+        ("prep", c_void_p),
     ]
 
 
@@ -103,6 +104,8 @@ _SIGNATURES = {
     "rq_dequantize": [_P, _P, c_size_t, _P, c_size_t, _P],
     "rq_affine_dequantize": [_P, _P, c_size_t, _P, _P, c_size_t, _P, c_size_t, c_uint32, c_uint32, _P],
     "rq_qweight_dequantize": [_P, POINTER(rq_qweight), _P, _P],
+    "rq_qweight_prep_bytes": [POINTER(rq_qweight)],
+    "rq_qweight_prepare": [_P, POINTER(rq_qweight), _P, c_size_t, _P],
     "rq_matmul": [_P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
     "rq_matmul_bt": [_P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
     "rq_matmul_at": [_P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
@@ -124,7 +127,8 @@ _SIGNATURES = {
     "rq_llama_tokens": [_P, POINTER(c_int32), c_int32, POINTER(c_int32), _P],
     "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }
-_RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p, "rq_qmatmul_lora_workspace": c_size_t}
+_RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p, "rq_qmatmul_lora_workspace": c_size_t,
+             "rq_qweight_prep_bytes": c_size_t}
 
 
 class RqError(RuntimeError):

@@ -53,6 +53,8 @@ int rq::check_qweight(const rq_qweight *w) {
         return fail(RQ_ERR_INVALID_ARGUMENT, "affine weight needs group > 0");
     if (n > 0 && !w->codes) return fail(RQ_ERR_INVALID_ARGUMENT, "null codes");
     if (w->n_out > 0 && !w->scales) return fail(RQ_ERR_INVALID_ARGUMENT, "null scales");
+    if (w->prep && (w->format != RQ_Q_AFFINE_U8 || !aligned(w->prep, 16)))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "a prepared table belongs to an affine weight and is 16-byte aligned");
     return RQ_OK;
 }
 
@@ -420,6 +422,27 @@ int rq_qweight_dequantize(rq_ctx *ctx, const rq_qweight *w, float *out, rq_strea
                                     false, pick(ctx, stream));
 }
 
+size_t rq_qweight_prep_bytes(const rq_qweight *w) {
+    if (!w || check_qweight(w) != RQ_OK) return 0;
+    return affine_prep_bytes(*w);
+}
+
+int rq_qweight_prepare(rq_ctx *ctx, rq_qweight *w, void *table, size_t table_bytes, rq_stream stream) {
+    RQ_ENTER(ctx);
+    if (!w) return fail(RQ_ERR_INVALID_ARGUMENT, "null weight");
+    w->prep = nullptr;
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    const size_t need = affine_prep_bytes(*w);
+    if (need == 0) return RQ_OK;  // nothing the GEMM would read
+    if (!table) return fail(RQ_ERR_INVALID_ARGUMENT, "null table");
+    if (!aligned(table, 16)) return fail(RQ_ERR_INVALID_ARGUMENT, "table must be 16-byte aligned");
+    if (table_bytes < need) return fail(RQ_ERR_SHAPE, "table of %zu bytes, the weight needs %zu", table_bytes, need);
+    if ((st = launch_affine_prep(*w, static_cast<float *>(table), pick(ctx, stream))) != RQ_OK) return st;
+    w->prep = static_cast<const float *>(table);
+    return RQ_OK;
+}
+
 static int matmul_common(rq_ctx *ctx, int variant, const float *a, const float *b, float *out, int64_t m,
                          int64_t k, int64_t n, rq_stream stream) {
     RQ_ENTER(ctx);
@@ -461,19 +484,20 @@ rq::GemmWorkspace rq::gemm_workspace(const rq_ctx *ctx, hipStream_t s) {
 // few tokens, the MFMA GEMM for many, the generic kernel for anything the
 // tuned paths do not serve.
 int rq::qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt,
-                            int64_t m, hipStream_t s) {
+                         int64_t m, const GemmWorkspace &ws, hipStream_t s) {
     if (w.k_in > 0) {
         // 1-2 tokens: the VALU dot2 GEMV; 3-16: the MFMA GEMV (measured faster
         // from 3 tokens on, e.g. 4096x4096 m = 4: 7.2 -> 6.3 us); the VALU
         // kernel also serves the 3-4 token shapes the MFMA kernel refuses
         // (affine codes).
         int st = RQ_ERR_UNSUPPORTED;
-        // f32 activations take the same kernels, rounded to fp16 as they load
+        // f32 activations take the same kernels, each value carried as two
+        // fp16 terms after a power-of-two scaling that keeps it in range
         if (m <= 2) st = launch_gemv_decode(w, x, xt, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 16) st = launch_gemv_mfma(w, x, xt, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 4 && xt == RQ_F16) st = launch_gemv_decode(w, x, xt, y, yt, (int)m, s);
         if (st == RQ_ERR_UNSUPPORTED && m <= 8) st = launch_gemv(w, x, xt, y, yt, (int)m, ctx->num_cus, s);
-        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, gemm_workspace(ctx, s), s);
+        if (st == RQ_ERR_UNSUPPORTED) st = launch_gemm(w, x, xt, y, yt, m, ctx->num_cus, ws, s);
         if (st != RQ_ERR_UNSUPPORTED) return st;
     }
     return launch_qlinear_generic(w, x, xt, y, yt, m, s);
@@ -525,8 +549,8 @@ int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, co
     }
     if (st == RQ_ERR_UNSUPPORTED) st = launch_swiglu_generic(gate, up, x, x_dtype, h, m, s);
     if (st != RQ_OK) return st;
-    // down projection of h
-    return qmatmul_dispatch(ctx, down, h, RQ_F16, y, y_dtype, m, s);
+    // down projection of h, with the same workspace
+    return qmatmul_dispatch(ctx, down, h, RQ_F16, y, y_dtype, m, ws, s);
 }
 
 extern "C" {
@@ -543,7 +567,8 @@ int rq_qmatmul(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype
     if (!mul_ok(m, w->k_in, &t) || !mul_ok(m, w->n_out, &t)) return fail(RQ_ERR_SHAPE, "shape overflows");
     if (m == 0 || w->n_out == 0) return RQ_OK;
     if (!y || (w->k_in > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
-    return qmatmul_dispatch(ctx, *w, x, x_dtype, y, y_dtype, m, pick(ctx, stream));
+    hipStream_t s = pick(ctx, stream);
+    return qmatmul_dispatch(ctx, *w, x, x_dtype, y, y_dtype, m, gemm_workspace(ctx, s), s);
 }
 
 int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, const rq_qweight *down, const void *x,

@@ -113,6 +113,10 @@ int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, cons
                          int num_cus, const GemmWorkspace &ws, hipStream_t s);
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s);
+// Bytes of the prefill GEMM's scale table of an affine weight (0: none), and
+// the launch that builds it (table[g][0][n] = s, table[g][1][n] = b - 1024 s).
+size_t affine_prep_bytes(const rq_qweight &w);
+int launch_affine_prep(const rq_qweight &w, float *table, hipStream_t s);
 // h = fp16(silu(X . deq(gate)^T) * (X . deq(up)^T)) in one GEMM launch, g and
 // u rounded to fp16 before the silu*mul (per-row int8, fp16 X, I % 8 == 0, a
 // grid that fills the device); RQ_ERR_UNSUPPORTED otherwise.
@@ -155,9 +159,10 @@ int launch_rope_scatter(const float *qkv, const float2 *rope, int p0, int n, int
 int launch_attn_prefill(const _Float16 *q, const _Float16 *kc, const _Float16 *vc, _Float16 *out, int p0, int n,
                         int n_heads, int n_kv, int hd, int max_seq, hipStream_t s);
 
-// Y = X . deq(W)^T over every kernel family, picked by m, dtypes and shape.
+// Y = X . deq(W)^T over every kernel family, picked by m, dtypes and shape;
+// the prefill GEMM may use ws (split-K partials, input preparation).
 int qmatmul_dispatch(rq_ctx *ctx, const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m,
-                     hipStream_t s);
+                     const GemmWorkspace &ws, hipStream_t s);
 
 // SwiGLU MLP: argument checks (weights, dtypes, shapes) and the launches over
 // a workspace h of 2*m*I fp16 values (see rq_mlp_swiglu).

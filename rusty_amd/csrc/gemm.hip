@@ -871,6 +871,29 @@ __global__ __launch_bounds__(256) void k_affine_prep(const float *__restrict__ s
     }
 }
 
+}  // namespace
+
+// Size of the prepared scale table of an affine weight the GEMM serves
+// (group a multiple of 64 dividing k_in, table addressable with 32-bit
+// offsets), else 0.
+size_t affine_prep_bytes(const rq_qweight &w) {
+    if (w.format != RQ_Q_AFFINE_U8 || w.group <= 0 || w.group % 64 != 0 || w.k_in <= 0 || w.n_out <= 0 ||
+        w.k_in % w.group != 0)
+        return 0;
+    const uint64_t b = (uint64_t)(w.k_in / w.group) * (uint64_t)w.n_out * 8u;
+    return b > 0xffffffffull ? 0 : (size_t)b;
+}
+
+int launch_affine_prep(const rq_qweight &w, float *table, hipStream_t s) {
+    const int64_t N = w.n_out, gpr = w.k_in / w.group;
+    hipLaunchKernelGGL(k_affine_prep, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(gpr, 64)), dim3(256), 0, s, w.scales,
+                       w.biases, (int)N, (int)gpr, table);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+namespace {
+
 // f32 activations to fp16 (round to nearest even), 8 per thread per step.
 __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, _Float16 *__restrict__ y, size_t n8) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
@@ -988,23 +1011,22 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
         return RQ_ERR_UNSUPPORTED;
     if (fmt == 1 && (w.group % 64 != 0 || K % w.group != 0)) return RQ_ERR_UNSUPPORTED;
     if (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)) return RQ_ERR_UNSUPPORTED;
+    if (!aligned(x, 16)) return RQ_ERR_UNSUPPORTED;
     const int64_t cus = num_cus > 0 ? num_cus : 256;
-    if (fmt == 0 && xt == RQ_F16) {
-        if (!aligned(x, 16)) return RQ_ERR_UNSUPPORTED;
-        return gemm_tiles(w, w.scales, 0, x, y, yt, m, cus, ws, s);
-    }
-    if (!ws.prep || (xt == RQ_F32 && !aligned(x, 16)) || (xt == RQ_F16 && !aligned(x, 16))) return RQ_ERR_UNSUPPORTED;
+    if (fmt == 0 && xt == RQ_F16) return gemm_tiles(w, w.scales, 0, x, y, yt, m, cus, ws, s);
+    // affine scales: the table prepared at load, else built here per call
+    const bool table = fmt == 1 && w.prep && affine_prep_bytes(w) > 0;
+    if (fmt == 1 && table && xt == RQ_F16) return gemm_tiles(w, w.prep, 1, x, y, yt, m, cus, ws, s);
+    if (!ws.prep) return RQ_ERR_UNSUPPORTED;
     uint8_t *prep = static_cast<uint8_t *>(ws.prep);
     size_t used = 0;
-    const float *scales = w.scales;
-    if (fmt == 1) {
-        const int64_t gpr = K / w.group;
-        const size_t sc_bytes = ((size_t)gpr * (size_t)N * 8 + 255) & ~size_t(255);
-        if (sc_bytes > ws.prep_bytes / 2) return RQ_ERR_UNSUPPORTED;
+    const float *scales = fmt == 1 && table ? w.prep : w.scales;
+    if (fmt == 1 && !table) {
+        const size_t sc_bytes = (affine_prep_bytes(w) + 255) & ~size_t(255);
+        if (sc_bytes == 0 || sc_bytes > ws.prep_bytes / 2) return RQ_ERR_UNSUPPORTED;
         float *sct = reinterpret_cast<float *>(prep);
-        hipLaunchKernelGGL(k_affine_prep, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(gpr, 64)), dim3(256), 0, s,
-                           w.scales, w.biases, (int)N, (int)gpr, sct);
-        RQ_LAUNCH_CHECK();
+        const int st = launch_affine_prep(w, sct, s);
+        if (st != RQ_OK) return st;
         scales = sct;
         used = sc_bytes;
     }

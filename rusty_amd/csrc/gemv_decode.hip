@@ -1,5 +1,5 @@
 // Decode dequant-GEMV, m <= 4:  Y[m, n] = sum_k X[m, k] * deq(W)[n, k], fp16
-// activations (f32 ones, m <= 2, rounded to fp16 as they are loaded).
+// activations (f32 ones, m <= 2, carried as two fp16 terms each: see XF).
 // Serves m = 1-2, and m = 3-4 for the weights the MFMA GEMV does not take
 // (affine codes); per-row codes at m >= 3 go to the MFMA GEMV.
 //
@@ -90,8 +90,13 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // split over positions): Xf holds acc[head][SA][attn_hd] (f32) followed by
 // (m, l)[head][SA] (float2); x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
 // M = max_s m_s, rounded to fp16 and shared through LDS like the norm's row.
-// XF (no NORM / SA): the activations are f32 (Xf), rounded to fp16 as they
-// are loaded.
+// XF (no NORM / SA): the activations are f32 (Xf).  Each 16-value chunk of a
+// row is scaled by a power of two 2^-e that puts its largest magnitude in
+// [2^14, 2^15) (exact), every scaled value is split into two fp16 terms
+// hi = fp16(v), lo = fp16(v - hi) (their sum equals v to ~2^-22 relative),
+// and the chunk's partial sums are multiplied back by 2^e: any finite f32
+// row is carried without overflowing fp16, and small values keep f32
+// accuracy instead of fp16's subnormal spacing.
 template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
@@ -122,8 +127,9 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     constexpr int XC = CPT * TPR;            // chunks the row groups cover
     constexpr int NL = (XC + DT - 1) / DT;   // NORM: chunks loaded per thread
     uint32_t xh[CPT][M][8];
-    // XF: x = xh + xl exactly to ~2^-22 relative (xh = fp16(x), xl = fp16(x - xh))
+    // XF: x = 2^e (xh + xl) to ~2^-22 relative, pe = 2^e per chunk and row
     uint32_t xl[XF ? CPT : 1][XF ? M : 1][8];
+    float pe[XF ? CPT : 1][XF ? M : 1];
     uint4 xf4[NORM ? NL : 1][4], nw4[NORM ? NL : 1][2];
     // SA: 8-element pieces of the row, piece u by thread u % DT: SA (m, l)
     // pairs of its head and SA x 8 accumulator values
@@ -174,10 +180,24 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                 uint4 f4[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) f4[q] = bload<0>(rx, off + 16 * q);
+                float amax = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    amax = fmaxf(fmaxf(fmaxf(amax, fabsf(__builtin_bit_cast(float, f4[q].x))),
+                                       fmaxf(fabsf(__builtin_bit_cast(float, f4[q].y)),
+                                             fabsf(__builtin_bit_cast(float, f4[q].z)))),
+                                 fabsf(__builtin_bit_cast(float, f4[q].w)));
+                // amax = f * 2^E, f in [0.5, 1): 2^-(E - 15) maps it into [2^14, 2^15)
+                // (a zero, infinite or NaN maximum gives E = 0: the values pass
+                // through scaled by 2^15 and an inf or NaN stays one)
+                const int ex = max(__builtin_amdgcn_frexp_expf(amax) - 15, -126);
+                pe[j][m] = __builtin_amdgcn_ldexpf(1.0f, ex);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float f[4] = {__builtin_bit_cast(float, f4[q].x), __builtin_bit_cast(float, f4[q].y),
-                                        __builtin_bit_cast(float, f4[q].z), __builtin_bit_cast(float, f4[q].w)};
+                    const float f[4] = {__builtin_amdgcn_ldexpf(__builtin_bit_cast(float, f4[q].x), -ex),
+                                        __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, f4[q].y), -ex),
+                                        __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, f4[q].z), -ex),
+                                        __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, f4[q].w), -ex)};
 #pragma unroll
                     for (int e = 0; e < 2; ++e) {
                         const h2_t h = {(_Float16)f[2 * e], (_Float16)f[2 * e + 1]};
@@ -380,6 +400,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             if constexpr (XF) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) s = dot2(xl[j][m][i], 0x3C003C00u, s);
+                s *= pe[j][m];
             }
             xs[j][m] = s;
             xs_tot[m] += s;
@@ -395,7 +416,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             const uint32_t wd[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
             float d[M];
 #pragma unroll
-            for (int m = 0; m < M; ++m) d[m] = FMT == 0 ? p[m] : 0.0f;
+            for (int m = 0; m < M; ++m) d[m] = FMT == 0 && !XF ? p[m] : 0.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t u = FMT == 0 ? (wd[q] ^ 0x80808080u) : wd[q];
@@ -421,12 +442,13 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
+                // XF: the chunk's sums are in units of 2^-e; pe = 2^e restores them
                 if constexpr (FMT == 0) {
-                    p[m] = d[m];
+                    p[m] = XF ? __builtin_fmaf(pe[j][m], d[m], p[m]) : d[m];
                 } else {
                     const float s = sg[r][j];
                     const float c = XF ? bg[r][j] : __builtin_fmaf(-1024.0f, s, bg[r][j]);
-                    p[m] = __builtin_fmaf(s, d[m], p[m]);
+                    p[m] = __builtin_fmaf(s, XF ? d[m] * pe[j][m] : d[m], p[m]);
                     p[m] = __builtin_fmaf(c, xs[j][m], p[m]);
                 }
             }

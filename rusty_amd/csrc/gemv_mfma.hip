@@ -110,17 +110,36 @@ __device__ __forceinline__ half8 u8x8_exact(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half8, r);
 }
 
-// 8 f32 values x -> hi = fp16(x), lo = fp16(x - hi) (round to nearest even):
-// hi + lo equals x to about 2^-22 relative.
-__device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 &hi, half8 &lo) {
-    const float f[8] = {__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, a.y), __builtin_bit_cast(float, a.z),
-                        __builtin_bit_cast(float, a.w), __builtin_bit_cast(float, b.x), __builtin_bit_cast(float, b.y),
-                        __builtin_bit_cast(float, b.z), __builtin_bit_cast(float, b.w)};
+// 8 f32 values x, scaled by 2^-sh (SC; exact) -> hi = fp16(x), lo =
+// fp16(x - hi) (round to nearest even): hi + lo equals x to about 2^-22
+// relative while |x| stays inside fp16's range.
+template <bool SC = false>
+__device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 &hi, half8 &lo, int sh = 0) {
+    float f[8] = {__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, a.y), __builtin_bit_cast(float, a.z),
+                  __builtin_bit_cast(float, a.w), __builtin_bit_cast(float, b.x), __builtin_bit_cast(float, b.y),
+                  __builtin_bit_cast(float, b.z), __builtin_bit_cast(float, b.w)};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
+        if constexpr (SC) f[e] = __builtin_amdgcn_ldexpf(f[e], -sh);
         hi[e] = (_Float16)f[e];
         lo[e] = (_Float16)(f[e] - (float)hi[e]);
     }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Maximum over the 64 lanes, uniform across the wave.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror: each 16-lane row holds its maximum
+    const auto rl = [](float x, int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+    };
+    return fmaxf(fmaxf(rl(v, 0), rl(v, 16)), fmaxf(rl(v, 32), rl(v, 48)));
 }
 
 // SWI: SwiGLU gate/up pass -- the block's 16 weight rows are 8 gate rows (W)
@@ -133,7 +152,11 @@ __device__ __forceinline__ void f32x8_split(const uint4 a, const uint4 b, half8 
 // XF: f32 activations (the reference's dtype), 32 bytes per lane per MFMA,
 // each split into two fp16 terms multiplied separately; per-row codes enter
 // as exact fp16 values, affine codes as exact u with the group's scale and
-// bias applied in f32 after the MFMAs (u . x and the group sum of x).
+// bias applied in f32 after the MFMAs (u . x and the group sum of x).  A
+// value past fp16's range makes its terms infinite and the batch's sums
+// non-finite; such a batch (any lane of the wave) is multiplied again with
+// every activation scaled by one wave-uniform power of two 2^-S that puts the
+// batch's largest magnitude in [2^14, 2^15), its sums scaled back by 2^S.
 // XFIRST: each batch's activation loads are issued before its weight loads
 // (see launch_mfma).
 template <bool SWI, int NWV, int FMT = 0, bool XF = false, bool XFIRST = false>
@@ -267,34 +290,79 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             const int c = 2 * j + (q >> 1);
             a[j] = *reinterpret_cast<const uint2 *>(wl + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
         }
-        if constexpr (FMT == 1 && XF) {
-            // exact: per group g (MFMAs 2 g, 2 g + 1), t = u . x and xs = sum x
-            // over the group (ones as the weight operand), then
-            // acc += s . t + b . xs in f32 for output rows 4 q + r
-            half8 ones;
+        if constexpr (XF) {
+            // f32 activations: the batch as loaded, then (rarely) again scaled
+            auto mma_x = [&](auto scaled, int sh) {
+                constexpr bool SC = decltype(scaled)::value;
+                if constexpr (FMT == 1) {
+                    // exact: per group g (MFMAs 2 g, 2 g + 1), t = u . x and xs =
+                    // sum x over the group (ones as the weight operand), then
+                    // acc += s . t + b . xs in f32 for output rows 4 q + r
+                    half8 ones;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+                    for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 #pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-                floatx4 tg = {0.0f, 0.0f, 0.0f, 0.0f}, xg = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int gi = 0; gi < 4; ++gi) {
+                        floatx4 tg = {0.0f, 0.0f, 0.0f, 0.0f}, xg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const int j = 2 * gi + jj;
-                    const half8 ue = u8x8_exact(a[j].x, a[j].y);
-                    half8 hi, lo;
-                    f32x8_split(b.x[2 * j], b.x[2 * j + 1], hi, lo);
-                    tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, hi, tg, 0, 0, 0);
-                    tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, lo, tg, 0, 0, 0);
-                    xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, hi, xg, 0, 0, 0);
-                    xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, lo, xg, 0, 0, 0);
+                        for (int jj = 0; jj < 2; ++jj) {
+                            const int j = 2 * gi + jj;
+                            const half8 ue = u8x8_exact(a[j].x, a[j].y);
+                            half8 hi, lo;
+                            f32x8_split<SC>(b.x[2 * j], b.x[2 * j + 1], hi, lo, sh);
+                            tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, hi, tg, 0, 0, 0);
+                            tg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ue, lo, tg, 0, 0, 0);
+                            xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, hi, xg, 0, 0, 0);
+                            xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, lo, xg, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr) {
+                            const float sv = gi == 0 ? b.s[rr].x : gi == 1 ? b.s[rr].y : gi == 2 ? b.s[rr].z : b.s[rr].w;
+                            const float bv = gi == 0 ? b.b[rr].x : gi == 1 ? b.b[rr].y : gi == 2 ? b.b[rr].z : b.b[rr].w;
+                            const float t = SC ? __builtin_amdgcn_ldexpf(tg[rr], sh) : tg[rr];
+                            const float xs = SC ? __builtin_amdgcn_ldexpf(xg[rr], sh) : xg[rr];
+                            acc[rr] = __builtin_fmaf(sv, t, acc[rr]);
+                            acc[rr] = __builtin_fmaf(bv, xs, acc[rr]);
+                        }
+                    }
+                } else {
+                    // x = hi + lo: the weight operand holds exact code values, so
+                    // the two products together keep f32 accuracy
+                    floatx4 t = acc;
+                    if constexpr (SC) t = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const half8 av = i8x8_to_half8(a[j].x, a[j].y);
+                        half8 hi, lo;
+                        f32x8_split<SC>(b.x[2 * j], b.x[2 * j + 1], hi, lo, sh);
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, hi, t, 0, 0, 0);
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, lo, t, 0, 0, 0);
+                    }
+                    if constexpr (SC) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[r] += __builtin_amdgcn_ldexpf(t[r], sh);
+                    } else {
+                        acc = t;
+                    }
                 }
+            };
+            const floatx4 acc0 = acc;
+            mma_x(std::false_type{}, 0);
+            const bool bad = !(__builtin_isfinite(acc[0]) && __builtin_isfinite(acc[1]) &&
+                               __builtin_isfinite(acc[2]) && __builtin_isfinite(acc[3]));
+            if (__builtin_amdgcn_ballot_w64(bad) != 0) {  // wave-uniform
+                float amax = 0.0f;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const float sv = gi == 0 ? b.s[rr].x : gi == 1 ? b.s[rr].y : gi == 2 ? b.s[rr].z : b.s[rr].w;
-                    const float bv = gi == 0 ? b.b[rr].x : gi == 1 ? b.b[rr].y : gi == 2 ? b.b[rr].z : b.b[rr].w;
-                    acc[rr] = __builtin_fmaf(sv, tg[rr], acc[rr]);
-                    acc[rr] = __builtin_fmaf(bv, xg[rr], acc[rr]);
-                }
+                for (int i = 0; i < 16; ++i)
+                    amax = fmaxf(fmaxf(amax, fmaxf(fabsf(__builtin_bit_cast(float, b.x[i].x)),
+                                                   fabsf(__builtin_bit_cast(float, b.x[i].y)))),
+                                 fmaxf(fabsf(__builtin_bit_cast(float, b.x[i].z)),
+                                       fabsf(__builtin_bit_cast(float, b.x[i].w))));
+                // amax = f * 2^E, f in [0.5, 1); an infinite maximum gives E = 0,
+                // and the infinity stays one
+                const int sh = __builtin_amdgcn_frexp_expf(wave_max(amax)) - 15;
+                acc = acc0;
+                mma_x(std::true_type{}, sh);
             }
             return;
         }
@@ -311,16 +379,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             half8 av;
             if constexpr (FMT == 1) av = u8x8_affine(a[j].x, a[j].y, sg[j / 2], cg[j / 2]);
             else av = i8x8_to_half8(a[j].x, a[j].y);
-            if constexpr (XF) {
-                // x = hi + lo: the weight operand holds exact code values, so
-                // the two products together keep f32 accuracy
-                half8 hi, lo;
-                f32x8_split(b.x[2 * j], b.x[2 * j + 1], hi, lo);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, hi, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, lo, acc, 0, 0, 0);
-            } else {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
-            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
         }
     };
 

@@ -530,7 +530,7 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
         st = c.head_dim == 64 ? launch_gemm_qkv_rope(L.qkv, md->pxn, n, ro, md->pq, md->ctx->num_cus, ws, s)
                               : RQ_ERR_UNSUPPORTED;
         if (st == RQ_ERR_UNSUPPORTED) {
-            if ((st = qmatmul_dispatch(md->ctx, L.qkv, md->pxn, RQ_F16, md->pqkv, RQ_F32, n, s))) return st;
+            if ((st = qmatmul_dispatch(md->ctx, L.qkv, md->pxn, RQ_F16, md->pqkv, RQ_F32, n, ws, s))) return st;
             if ((st = launch_rope_scatter(md->pqkv, md->rope, p0, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
                                           md->pq, kc, vc, s)))
                 return st;
@@ -541,7 +541,7 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
         if ((st = launch_attn_prefill(md->pq, kc, vc, md->patt, p0, n, c.n_heads, c.n_kv_heads, c.head_dim,
                                       c.max_seq, s)))
             return st;
-        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt, RQ_F16, md->py, RQ_F32, n, s))) return st;
+        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt, RQ_F16, md->py, RQ_F32, n, ws, s))) return st;
         if ((st = launch_add_rmsnorm_rows(md->px, md->py, L.mlp_norm, c.norm_eps, md->pxn, n, H, s))) return st;
         if ((st = swiglu_run(md->ctx, L.gate, L.up, L.down, md->pxn, RQ_F16, md->ph, md->py, RQ_F32, n, ws, s)))
             return st;
@@ -560,7 +560,7 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
                                       c.max_seq, s)))
             return st;
         const size_t last = (size_t)(n - 1);
-        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt + last * qrow, RQ_F16, md->py + last * H, RQ_F32, 1, s)))
+        if ((st = qmatmul_dispatch(md->ctx, L.o, md->patt + last * qrow, RQ_F16, md->py + last * H, RQ_F32, 1, ws, s)))
             return st;
         if ((st = launch_add_rmsnorm_rows(md->px + last * H, md->py + last * H, L.mlp_norm, c.norm_eps,
                                           md->pxn + last * H, 1, H, s)))
@@ -582,7 +582,36 @@ int prefill_chunk(rq_llama *md, int p0, int n, bool end, hipStream_t s) {
     return RQ_OK;
 }
 
+// Captures the decode step into a graph on stream s and instantiates it, the
+// first time a step runs in graph mode (a runner that steps eagerly never
+// captures one).  The step's kernels use no context workspace, so the graph
+// may be replayed on any stream.
+int ensure_graph(rq_llama *md, hipStream_t s) {
+    if (md->exec) return RQ_OK;
+    RQ_HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int st = enqueue_step(md, s);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &g);
+    if (st != RQ_OK || e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return st != RQ_OK ? st : fail(RQ_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    }
+    hipGraphExec_t x = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(RQ_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ei));
+    }
+    md->graph = g;
+    md->exec = x;
+    return RQ_OK;
+}
+
 int run_steps(rq_llama *md, int n, hipStream_t s) {
+    if (md->use_graph && n > 0) {
+        const int st = ensure_graph(md, s);
+        if (st != RQ_OK) return st;
+    }
     for (int i = 0; i < n; ++i) {
         if (md->use_graph) {
             RQ_HIP_TRY(hipGraphLaunch(md->exec, s));
@@ -659,10 +688,21 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
     auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
     std::vector<size_t> per_row(L);  // scale entries per row of each layer's q/k/v
     size_t bytes = 0;
-    for (size_t l = 0; l < L; ++l) {
+    // Affine Linears: the prefill GEMM's scale tables (load-time preparation),
+    // built here for the packed q/k/v and for any borrowed Linear that comes
+    // without one.
+    auto qkv_of = [&](size_t l) {
         const rq_qweight &q = w->layers[l].q;
+        return rq_qweight{q.codes, q.scales, q.biases, QKV, H, q.format, q.group, nullptr};
+    };
+    auto table_bytes = [&](const rq_qweight &lw) { return lw.prep ? 0 : affine_prep_bytes(lw); };
+    for (size_t l = 0; l < L; ++l) {
+        const rq_llama_layer &src = w->layers[l];
+        const rq_qweight &q = src.q;
         per_row[l] = q.format == RQ_Q_AFFINE_U8 ? (size_t)(H / q.group) : 1;
         bytes += pad((size_t)QKV * H) + pad((size_t)QKV * per_row[l] * 4) * (q.biases ? 2 : 1);
+        bytes += pad(affine_prep_bytes(qkv_of(l))) + pad(table_bytes(src.o)) + pad(table_bytes(src.gate)) +
+                 pad(table_bytes(src.up)) + pad(table_bytes(src.down));
     }
     // attention splits: ~160 positions of the cache per block up to 480 (each
     // block's K/V rows stream through one CU), 8 beyond (for 640 positions 8
@@ -708,11 +748,22 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
             }
             row += n;
         }
-        dst.qkv = rq_qweight{codes, scales, biases, QKV, H, src.q.format, src.q.group};
+        dst.qkv = rq_qweight{codes, scales, biases, QKV, H, src.q.format, src.q.group, nullptr};
         dst.o = src.o;
         dst.gate = src.gate;
         dst.up = src.up;
         dst.down = src.down;
+        // scale tables (stream-ordered after the q/k/v packing above)
+        for (rq_qweight *lw : {&dst.qkv, &dst.o, &dst.gate, &dst.up, &dst.down}) {
+            const size_t tb = lw->prep ? 0 : affine_prep_bytes(*lw);
+            if (tb == 0) continue;
+            float *table = carve<float>(p, tb / 4);
+            if ((st = launch_affine_prep(*lw, table, s)) != RQ_OK) {
+                release(md);
+                return st;
+            }
+            lw->prep = table;
+        }
         dst.attn_norm = static_cast<const _Float16 *>(src.attn_norm);
         dst.mlp_norm = static_cast<const _Float16 *>(src.mlp_norm);
     }
@@ -753,26 +804,6 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
         return fail(RQ_ERR_HIP, "packing q/k/v: %s", hipGetErrorString(e));
     }
 
-    // capture one step; the graph holds kernel launches only
-    e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
-    if (e != hipSuccess) {
-        release(md);
-        return fail(RQ_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
-    }
-    st = enqueue_step(md, s);
-    hipGraph_t g = nullptr;
-    e = hipStreamEndCapture(s, &g);
-    md->graph = g;
-    if (st != RQ_OK || e != hipSuccess) {
-        release(md);
-        return st != RQ_OK ? st : fail(RQ_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
-    }
-    e = hipGraphInstantiate(&md->exec, md->graph, nullptr, nullptr, 0);
-    if (e != hipSuccess) {
-        md->exec = nullptr;
-        release(md);
-        return fail(RQ_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-    }
     *out = md;
     return RQ_OK;
 }

@@ -135,7 +135,7 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
     }
     if (st != RQ_OK) return st;
     // the fused dequant product, f32
-    if ((st = qmatmul_dispatch(ctx, *w, x, x_dtype, mainv, RQ_F32, m, s)) != RQ_OK) return st;
+    if ((st = qmatmul_dispatch(ctx, *w, x, x_dtype, mainv, RQ_F32, m, gemm_workspace(ctx, s), s)) != RQ_OK) return st;
     // y = main + t . B [m, n_out]: enough row groups for ~4 blocks per CU,
     // each thread's B column read once per row group
     const int64_t gxl = cdiv(N, TH);

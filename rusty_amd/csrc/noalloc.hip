@@ -73,7 +73,8 @@ extern "C" int rq_mlp_swiglu_noalloc(rq_ctx *ctx, const rq_qweight *gate, const 
                         ctx->device >= 0 && ctx->device < kMaxDevices ? hipGetErrorString(g_scratch_err[ctx->device])
                                                                       : "device ordinal out of range");
     }
-    // no split-K: the context's split-K workspace is not shared with these calls
+    // no workspace for any of its GEMMs (gate/up and down): the context's
+    // split-K partials and preparation area are not shared with these calls
     const GemmWorkspace none{nullptr, nullptr, 0, 0};
     return swiglu_run(ctx, *gate, *up, *down, x, x_dtype, h, y, y_dtype, m, none, pick(ctx, stream));
 }

@@ -190,6 +190,7 @@ class QuantizedTensor:
     k_in: int
     format: int
     group: int
+    prep: UnifiedTensor | None = None  # affine: the prefill GEMM's scale table (rq_qweight_prepare)
 
     @classmethod
     def rowwise(cls, ctx: WgpuContext, q: np.ndarray, scales: np.ndarray) -> "QuantizedTensor":
@@ -202,9 +203,12 @@ class QuantizedTensor:
 
     @classmethod
     def affine(cls, ctx: WgpuContext, u: np.ndarray, scales: np.ndarray, biases: np.ndarray | None,
-               group: int = 64) -> "QuantizedTensor":
+               group: int = 64, prepare: bool = True) -> "QuantizedTensor":
         """The reference's affine format: unsigned codes ``u[n_out, k_in]``,
-        f32 scale and bias per ``group`` consecutive flat elements."""
+        f32 scale and bias per ``group`` consecutive flat elements.  With
+        ``prepare`` the prefill GEMM's scale table is built once here (load
+        time, as upload_quantized does its one-time work), so no GEMM call
+        rebuilds it."""
         u = np.ascontiguousarray(u, dtype=np.uint8)
         n, k = u.shape
         s = UnifiedTensor.new(ctx, np.ascontiguousarray(scales, dtype=np.float32).ravel(), dtype=DType.FP32)
@@ -213,11 +217,28 @@ class QuantizedTensor:
         need = -(-n * k // group)
         if s.numel < need or (b is not None and b.numel < need):
             raise ValueError(f"{n}x{k} weight with group {group} needs {need} scales/biases")
-        return cls(UnifiedTensor.new(ctx, u, dtype=DType.U8), s, b, n, k, _lib.RQ_Q_AFFINE_U8, group)
+        qt = cls(UnifiedTensor.new(ctx, u, dtype=DType.U8), s, b, n, k, _lib.RQ_Q_AFFINE_U8, group)
+        if prepare:
+            qt.prepare(ctx)
+        return qt
+
+    def prepare(self, ctx: WgpuContext, stream=None) -> None:
+        """Builds the prefill GEMM's scale table of an affine weight
+        (rq_qweight_prepare); nothing for weights that need none."""
+        d = self.descriptor()
+        d.prep = None
+        nbytes = int(_lib.lib().rq_qweight_prep_bytes(ctypes.byref(d)))
+        if nbytes == 0:
+            self.prep = None
+            return
+        table = UnifiedTensor.empty(ctx, [nbytes // 4], DType.FP32)
+        call("rq_qweight_prepare", ctx.handle, ctypes.byref(d), table.ptr, nbytes, _stream(stream))
+        self.prep = table
 
     def descriptor(self) -> rq_qweight:
         return rq_qweight(self.codes.ptr, self.scales.ptr, self.biases.ptr if self.biases is not None else None,
-                          self.n_out, self.k_in, self.format, self.group)
+                          self.n_out, self.k_in, self.format, self.group,
+                          self.prep.ptr if self.prep is not None else None)
 
 
 _XDT = {DType.FP32: _lib.RQ_F32, DType.FP16: _lib.RQ_F16}

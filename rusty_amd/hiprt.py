@@ -1,7 +1,8 @@
 """Minimal ctypes access to the HIP runtime that librusty_hip.so links.
 
-Timing (hipEvent*) and stream capture into HIP graphs (hipStreamBeginCapture
-... hipGraphLaunch) for the benchmark and the graph-replay tests.  The
+Timing (hipEvent*), extra streams (default priority) and stream capture into
+HIP graphs (hipStreamBeginCapture ... hipGraphLaunch) for the benchmark and
+the graph-replay tests.  The
 runtime is the same ``libamdhip64.so.7`` instance the library loaded.
 """
 from __future__ import annotations
@@ -35,6 +36,8 @@ def hip() -> ctypes.CDLL:
             "hipGraphExecDestroy": [P],
             "hipGraphDestroy": [P],
             "hipStreamSynchronize": [P],
+            "hipStreamCreateWithFlags": [POINTER(c_void_p), ctypes.c_uint],
+            "hipStreamDestroy": [P],
             "hipDeviceSynchronize": [],
             "hipGetErrorString": [c_int],
         }
@@ -71,6 +74,26 @@ class Event:
         try:
             if self.h:
                 hip().hipEventDestroy(self.h)
+        except Exception:
+            pass
+
+
+class Stream:
+    """A non-blocking HIP stream of default priority (streams of other
+    priorities are not used)."""
+
+    def __init__(self):
+        self.h = c_void_p()
+        _ok(hip().hipStreamCreateWithFlags(byref(self.h), 1), "hipStreamCreateWithFlags")
+
+    def synchronize(self) -> None:
+        _ok(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
+
+    def __del__(self):
+        try:
+            if self.h:
+                hip().hipStreamSynchronize(self.h)
+                hip().hipStreamDestroy(self.h)
         except Exception:
             pass
 

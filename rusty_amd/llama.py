@@ -52,10 +52,14 @@ class LlamaConfig:
                 "gate": (self.intermediate, self.hidden), "up": (self.intermediate, self.hidden),
                 "down": (self.hidden, self.intermediate)}
 
-    def weight_bytes(self) -> int:
-        """Int8 code bytes + f32 scale bytes read by one decode step."""
-        per_layer = sum(n * k + 4 * n for n, k in self.linear_shapes().values())
-        return self.n_layers * per_layer + self.vocab * self.hidden + 4 * self.vocab
+    def weight_bytes(self, affine_group: int = 0) -> int:
+        """Code bytes + f32 scale (and bias) bytes read by one decode step:
+        per-row int8 (one scale per row), or with ``affine_group`` the
+        reference's affine u8 codes (an f32 scale and bias per group)."""
+        def lin(n, k):
+            return n * k + (8 * n * (k // affine_group) if affine_group else 4 * n)
+        per_layer = sum(lin(n, k) for n, k in self.linear_shapes().values())
+        return self.n_layers * per_layer + lin(self.vocab, self.hidden)
 
 
 # configs[4]: the 1.1B shape (22 layers, hidden 2048, 32/4 heads of 64,
@@ -75,17 +79,26 @@ class LlamaHostWeights:
     lm_head: tuple[np.ndarray, np.ndarray] | None = None
 
 
-def synth_weights(cfg: LlamaConfig, seed: int = 0) -> LlamaHostWeights:
+def synth_weights(cfg: LlamaConfig, seed: int = 0, affine_group: int = 0) -> LlamaHostWeights:
     """Random-init weights of the architecture (no checkpoint is available).
 
     Linear codes uniform in [-127, 127] with per-row scales ~ U(1.36e-4, 4.09e-4):
     the dequantized weights have std ~0.02, the usual Llama init, so
-    activations stay O(1) through the layers.  Norm weights 1 + U(-0.1, 0.1),
-    embeddings N(0, 1); all fp16.
+    activations stay O(1) through the layers.  With ``affine_group`` every
+    Linear (lm_head included) is in the reference's affine u8 format instead:
+    codes uniform in [0, 255], per group of ``affine_group`` along k an f32
+    scale ~ U(0.5, 1.5) * 0.02 / 73.3 and bias -128 * scale * U(0.98, 1.02)
+    (an MLX checkpoint's shape of values; std ~0.02 around zero).  Norm
+    weights 1 + U(-0.1, 0.1), embeddings N(0, 1); all fp16.
     """
     g = np.random.default_rng(seed)
 
     def linear(n, k):
+        if affine_group:
+            u = g.integers(0, 256, size=(n, k), dtype=np.uint8)
+            sc = g.uniform(0.5, 1.5, size=(n, k // affine_group)) * (0.02 / 73.3)
+            b = (-128.0 * sc * g.uniform(0.98, 1.02, size=sc.shape)).astype(np.float32)
+            return u, sc.astype(np.float32), b, affine_group
         q = g.integers(-127, 128, size=(n, k), dtype=np.int8)
         s = g.uniform(0.02 / 73.3 * 0.5, 0.02 / 73.3 * 1.5, size=n).astype(np.float32)
         return q, s
@@ -129,8 +142,15 @@ def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaH
     embedding is tied to the lm_head (:242-249).  The runner's embedding table
     is fp16: a quantized ``model.embed_tokens`` is dequantized on the host
     (u * s + b in f64) and rounded to fp16, norms are rounded to fp16.
-    ``max_seq`` defaults to ``max_position_embeddings`` (else 2048), capped at
-    the runner's 32768 positions."""
+    A checkpoint with ``model.embedding_norm`` has that RMSNorm applied to the
+    embedding rows before the first layer (Lfm2Model::forward,
+    rusty-graph/src/lfm.rs:121-122): the norm is row-wise and a lookup selects
+    rows, so the table is normalised once here, in f64 from the unrounded
+    rows -- x / sqrt(mean(x^2) + eps) * w -- and then rounded to fp16; the
+    tied lm_head keeps the checkpoint's own codes (lfm.rs builds it from the
+    raw embedding weight, model_builder.rs:242-249).  ``max_seq`` defaults to
+    ``max_position_embeddings`` (else 2048), capped at the runner's 32768
+    positions."""
     from pathlib import Path
 
     from .loader import LoaderError, QuantizationConfig, WeightsContext, load_config
@@ -183,11 +203,15 @@ def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaH
             codes, sc, b, gs = quantized("model.embed_tokens")
             tied = (codes, sc, b, gs)
             rep = lambda a: np.repeat(a.astype(np.float64), gs, axis=1)  # noqa: E731
-            embed = (codes * rep(sc) + rep(b)).astype(np.float16)
+            embed = codes * rep(sc) + rep(b)
         else:
             tied = None
-            embed = plain("model.embed_tokens").astype(np.float16)
-        w = LlamaHostWeights(embed=embed.reshape(cfg.vocab, cfg.hidden))
+            embed = plain("model.embed_tokens").astype(np.float64)
+        embed = embed.reshape(cfg.vocab, cfg.hidden)
+        if wc.get_tensor_info("model.embedding_norm.weight") is not None:
+            nw = plain("model.embedding_norm").astype(np.float64)
+            embed = embed / np.sqrt((embed * embed).mean(axis=1, keepdims=True) + cfg.norm_eps) * nw
+        w = LlamaHostWeights(embed=embed.astype(np.float16))
         for i in range(cfg.n_layers):
             pre = f"model.layers.{i}"
             layer = {}

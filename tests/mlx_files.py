@@ -21,11 +21,12 @@ def _enc(a, dt):
 
 
 def write_mlx_llama(path, cfg, seed=0, names="reference", tie=True, quant_embed=True, sdt="BF16", group=64,
-                    files=2):
+                    files=2, embedding_norm="random"):
     """cfg: a LlamaConfig.  Codes uniform in [0, 255]; scales ~ U(0.5, 1.5) *
     0.02 / 73.3 per group and biases ~ -128 * scale, so the weights have
     std ~0.02 around zero; norm weights 1 + U(-0.1, 0.1).  Tensors are spread
-    over ``files`` safetensors files."""
+    over ``files`` safetensors files.  ``embedding_norm``: "random" (norm
+    weights as above), "ones" (all 1.0) or None (no model.embedding_norm)."""
     g = np.random.default_rng(seed)
     nm = dict(REFERENCE_NAMES if names == "reference" else MLX_NAMES)
     nm.update(q="self_attn.q_proj", k="self_attn.k_proj", v="self_attn.v_proj")
@@ -52,7 +53,10 @@ def write_mlx_llama(path, cfg, seed=0, names="reference", tie=True, quant_embed=
         norm(f"{pre}.{nm['mlp_norm']}")
         for key, (n, k) in cfg.linear_shapes().items():
             quant(f"{pre}.{nm[key]}", n, k)
-    norm("model.embedding_norm")
+    if embedding_norm == "ones":
+        tensors["model.embedding_norm.weight"] = (sdt, _enc(np.ones(cfg.hidden), sdt))
+    elif embedding_norm is not None:
+        norm("model.embedding_norm")
     if names != "reference":
         norm("model.norm")
     if not tie:

@@ -43,10 +43,38 @@ def test_null_arguments_rejected_without_device():
     assert lib.rq_ctx_destroy(None) == _lib.RQ_OK
 
 
-def test_struct_layout_matches_header():
-    # rq_qweight: 3 pointers, 2 int64, 2 int32 -> 48 bytes, no padding surprises
-    assert ctypes.sizeof(_lib.rq_qweight) == 48
-    assert _lib.rq_qweight.n_out.offset == 24 and _lib.rq_qweight.format.offset == 40
+def test_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors have the sizes and field offsets a C compiler gives
+    the header's structs (compiled and printed by gcc)."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    root = Path(__file__).resolve().parent.parent
+    src = tmp_path / "layout.c"
+    src.write_text("""#include <stdio.h>
+#include <stddef.h>
+#include "rusty_hip.h"
+int main(void) {
+    printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(rq_qweight), offsetof(rq_qweight, n_out),
+           offsetof(rq_qweight, format), offsetof(rq_qweight, group), offsetof(rq_qweight, prep),
+           sizeof(rq_llama_layer));
+    printf("%zu %zu %zu\\n", sizeof(rq_llama_config), sizeof(rq_llama_weights), offsetof(rq_llama_weights, lm_head));
+    return 0;
+}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", "-I", str(root / "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    q = _lib.rq_qweight
+    assert [int(v) for v in out] == [ctypes.sizeof(q), q.n_out.offset, q.format.offset, q.group.offset,
+                                     q.prep.offset, ctypes.sizeof(_lib.rq_llama_layer),
+                                     ctypes.sizeof(_lib.rq_llama_config), ctypes.sizeof(_lib.rq_llama_weights),
+                                     _lib.rq_llama_weights.lm_head.offset]
+    assert ctypes.sizeof(q) == 56  # 3 pointers, 2 int64, 2 int32, the table pointer
 
 
 def _build_c_example(tmp_path):

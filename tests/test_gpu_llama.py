@@ -193,6 +193,26 @@ def test_llama_1b_128_greedy_steps(ctx):
     check_steps(cfg, w, toks, logits, 512, 2e-2, "1B")
 
 
+def test_llama_1b_affine_128_greedy_steps(ctx):
+    """configs[4] on the reference's own weight format: every Linear of the
+    22-layer 1.1B model (lm_head included) as affine u8 codes with an f32
+    scale and bias per 64 (what rusty-loader's upload_quantized reads,
+    rusty-loader/src/lib.rs:155-218); 512-token prompt through the batched
+    prefill (the affine GEMMs on their load-time scale tables), then 128
+    greedy steps on the affine decode GEMVs, every step's logits and token
+    against the oracle."""
+    cfg = LLAMA_1B
+    w = synth_weights(cfg, seed=3, affine_group=64)
+    assert len(w.layers[0]["gate"]) == 4 and len(w.lm_head) == 4
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 512)
+    r = LlamaRunner(ctx, cfg, w)
+    toks, logits = run_collect(r, prompt, 127)
+    r.close()
+    assert toks.shape == (640,) and logits.shape == (128, cfg.vocab)
+    np.testing.assert_array_equal(toks[:512], prompt)
+    check_steps(cfg, w, toks, logits, 512, 2e-2, "1B affine")
+
+
 @pytest.mark.parametrize("cfg,n_prompt", [
     (LlamaConfig(n_layers=1, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=256, vocab=300,
                  max_seq=1100), 1030),

@@ -154,6 +154,39 @@ def test_gemv_f32_output_and_activations(ctx, engine, ydt):
 # fp16 terms (hi + lo equals it to ~2^-22) and the weights enter as exact code
 # values (affine: u, with the group's scale and bias applied in f32), so the
 # result keeps f32 accuracy: the f32 bar (1e-5 of max|y|).
+# f32 activations outside fp16's range: every row holds a few entries of
+# 1e5..3e5 (fp16 ends at 65504), so a plain fp16 hi/lo split would give inf
+# and NaN rows.  The dot2 GEMV (m <= 2) scales each 16-value chunk by a power
+# of two before splitting; the MFMA GEMV redoes a batch whose sums come out
+# non-finite with its activations scaled by a power of two.  Checked per row
+# against the f64 truth at the f32 bar (a row's error over its own max|y|).
+# m = 2 also carries a row of values ~1e-6 (below fp16's normal range), which
+# the per-chunk scaling keeps at f32 accuracy.
+@pytest.mark.parametrize("m,fmt", [(1, 0), (2, 0), (4, 0), (12, 0), (1, 1), (2, 1), (4, 1), (12, 1)])
+def test_f32_activations_past_fp16_range(ctx, engine, m, fmt):
+    g = synth.rng(950 + 16 * m + fmt)
+    n, k = 1024, 4096
+    x = synth.activations(g, m, k, dtype=np.float32)
+    for r in range(m):
+        j = g.choice(k, size=3, replace=False)
+        x[r, j] = (g.choice([-1.0, 1.0], 3) * g.uniform(1e5, 3e5, 3)).astype(np.float32)
+    if m == 2:
+        x[1] = (synth.activations(g, 1, k, dtype=np.float32)[0] * 1e-6).astype(np.float32)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n, k)
+        b, W = None, QuantizedTensor.rowwise(ctx, q, s)
+    else:
+        q, s, b = synth.affine_weight(g, n, k)
+        W = QuantizedTensor.affine(ctx, q, s, b)
+    truth = orc.qlinear_truth(q, s, b, x, fmt)
+    y = qmm(ctx, engine, W, x, np.float32)
+    assert np.isfinite(y).all()
+    for r in range(m):
+        max_abs, rel, ok = f32_norm_check(y[r], truth[r])
+        report(f"f32 x wide range m={m} row {r} fmt={fmt}", max_abs, rel)
+        assert ok
+
+
 @pytest.mark.parametrize("m,n,k,fmt", [(1, 4096, 4096, 0), (2, 4096, 4096, 0), (3, 1000, 2048, 0),
                                        (4, 4096, 4096, 0), (8, 1024, 1024, 0), (16, 4096, 4096, 0),
                                        (5, 333, 4096, 0), (1, 11008, 4096, 0), (1, 4096, 11008, 0),
@@ -303,6 +336,69 @@ def test_config4_prefill_affine(ctx, engine, xdt):
     y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float16)
     assert np.isfinite(y).all()
     _check_rows(y, x, (u, s, b, 1, 64), f"C4 affine g64 2048x4096x4096 x={np.dtype(xdt).name}")
+
+
+# The scale table built once per weight at load (rq_qweight_prepare, what
+# QuantizedTensor.affine does by default) is the table the GEMM otherwise
+# builds in the context's preparation area on every call: the two give the
+# same bits.  A prepared weight needs no context area, so with fp16
+# activations it also runs the fast GEMM on another stream (the same bits
+# where the context stream does not split K).
+@pytest.mark.parametrize("m,n,k,group", [(2048, 4096, 4096, 64), (300, 4096, 1024, 128), (17, 300, 1024, 64),
+                                         (1500, 4100, 1088, 64)])
+def test_affine_prepared_table_matches_per_call(ctx, engine, m, n, k, group):
+    from rusty_amd.hiprt import Stream
+
+    g = synth.rng(5000 + m + k + group)
+    u, s, b = _affine(g, n, k, group)
+    x = synth.activations(g, m, k, sigma=0.5)
+    wp = QuantizedTensor.affine(ctx, u, s, b, group)
+    wn = QuantizedTensor.affine(ctx, u, s, b, group, prepare=False)
+    assert wp.prep is not None and wp.prep.numel * 4 == 8 * n * (k // group) and wn.prep is None
+    yp = qmm(ctx, engine, wp, x, np.float16)
+    yn = qmm(ctx, engine, wn, x, np.float16)
+    np.testing.assert_array_equal(yp.view(np.uint16), yn.view(np.uint16))
+    if m >= 256:  # no split-K on the context stream either
+        st = Stream()
+        X = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+        Y = UnifiedTensor.new(ctx, np.full((m, n), np.nan, np.float16), dtype=DType.FP16)
+        engine.qmatmul(ctx, X, wp, Y, stream=st.h)
+        st.synchronize()
+        np.testing.assert_array_equal(Y.to_vec().view(np.uint16), yp.view(np.uint16))
+    _check_rows(yp, x, (u, s, b, 1, group), f"prepared affine {m}x{n}x{k} g={group}")
+
+
+def test_qweight_prepare_arguments(ctx):
+    import ctypes
+
+    from rusty_amd import _lib
+
+    g = synth.rng(5100)
+    q, s = synth.rowwise_weight(g, 64, 256)
+    wr = QuantizedTensor.rowwise(ctx, q, s)
+    d = wr.descriptor()
+    assert _lib.lib().rq_qweight_prep_bytes(ctypes.byref(d)) == 0  # per-row: nothing to prepare
+    _lib.call("rq_qweight_prepare", ctx.handle, ctypes.byref(d), None, 0, None)
+    assert not d.prep
+    u, s, b = _affine(g, 64, 256)
+    wa = QuantizedTensor.affine(ctx, u, s, b, prepare=False)
+    d = wa.descriptor()
+    assert _lib.lib().rq_qweight_prep_bytes(ctypes.byref(d)) == 8 * 64 * 4
+    t = UnifiedTensor.empty(ctx, [511], DType.FP32)
+    with pytest.raises(RqError, match="RQ_ERR_SHAPE"):
+        _lib.call("rq_qweight_prepare", ctx.handle, ctypes.byref(d), t.ptr, 511 * 4, None)
+    assert not d.prep
+    # group 16 serves the decode kernels only: nothing to prepare
+    u, s, b = _affine(g, 64, 256, 16)
+    d = QuantizedTensor.affine(ctx, u, s, b, 16).descriptor()
+    assert _lib.lib().rq_qweight_prep_bytes(ctypes.byref(d)) == 0 and not d.prep
+    # a table on a per-row weight is refused
+    d = wr.descriptor()
+    d.prep = t.ptr
+    Y = UnifiedTensor.empty(ctx, [1, 64], DType.FP32)
+    X = UnifiedTensor.new(ctx, synth.activations(g, 1, 256), dtype=DType.FP16)
+    with pytest.raises(RqError, match="RQ_ERR_INVALID_ARGUMENT"):
+        _lib.call("rq_qmatmul", ctx.handle, ctypes.byref(d), X.ptr, _lib.RQ_F16, Y.ptr, _lib.RQ_F32, 1, None)
 
 
 def test_config4_prefill_f32_activations(ctx, engine):

@@ -4,7 +4,9 @@ affine linear -- no GPU.
 load_mlx follows the reference's ModelBuilder (rusty-graph/src/model_builder.rs):
 quantized weights are those with a ``.scales`` tensor, the final norm falls back
 to ``model.embedding_norm``, and without ``lm_head.weight`` the embedding is
-tied to the lm_head.  The expected values come from the writer's own tensors
+tied to the lm_head.  ``model.embedding_norm`` is also applied to the
+embedding rows before the first layer (Lfm2Model::forward,
+rusty-graph/src/lfm.rs:121-122), so the runner's table holds normalised rows.  The expected values come from the writer's own tensors
 and from the C restatement of affine_dequantize (oracle/oracle.py), not from
 load_mlx's code.
 """
@@ -53,20 +55,50 @@ def test_reference_names_tied_quantized_embed(tmp_path):
                                   _widen("BF16", t["model.embedding_norm.weight"][1]).astype(np.float16))
     # tied: the lm_head is the quantized embedding
     np.testing.assert_array_equal(w.lm_head[0], _codes(t["model.embed_tokens.weight"][1], CFG.vocab))
-    # the fp16 embedding table is the dequantized embedding (within one fp16 rounding of the f32 result)
+    # the fp16 embedding table is the dequantized embedding (C restatement of
+    # the reference kernel) after the embedding RMSNorm: each row divided by
+    # sqrt(|row|^2 / H + eps) and scaled by the norm weight, within one fp16
+    # rounding (these rows have mean square ~4e-4, so eps = 1e-5 moves them by ~1 %)
     deq = orc.affine_dequantize(_codes(t["model.embed_tokens.weight"][1], CFG.vocab),
                                 _widen("BF16", t["model.embed_tokens.scales"][1]),
                                 _widen("BF16", t["model.embed_tokens.biases"][1]), group=64)
+    deq = deq.reshape(CFG.vocab, CFG.hidden).astype(np.float64)
+    rms = np.sqrt(np.linalg.norm(deq, axis=1, keepdims=True) ** 2 / CFG.hidden + CFG.norm_eps)
+    nw = _widen("BF16", t["model.embedding_norm.weight"][1]).astype(np.float64)
     assert w.embed.dtype == np.float16 and w.embed.shape == (CFG.vocab, CFG.hidden)
-    np.testing.assert_allclose(w.embed.astype(np.float32), deq.reshape(CFG.vocab, CFG.hidden), rtol=2 ** -10,
-                               atol=2 ** -24)
+    np.testing.assert_allclose(w.embed.astype(np.float64), deq / rms * nw, rtol=2 ** -10, atol=1e-4)
+
+
+def test_embedding_norm_applied_at_input(tmp_path):
+    # all-ones norm weight: every row of the table has root mean square 1
+    # (eps = 1e-5 against rows of mean square ~0.9 moves it by < 1e-5)
+    write_mlx_llama(tmp_path, CFG, seed=6, tie=False, quant_embed=False, embedding_norm="ones", files=1)
+    _, w = load_mlx(tmp_path)
+    rms = np.sqrt((w.embed.astype(np.float64) ** 2).mean(axis=1))
+    np.testing.assert_allclose(rms, 1.0, atol=1e-3)
+    # without model.embedding_norm the table is the stored one, unnormalised
+    t = write_mlx_llama(tmp_path, CFG, seed=6, tie=False, quant_embed=False, embedding_norm=None, names="mlx", files=1)
+    _, w = load_mlx(tmp_path)
+    np.testing.assert_array_equal(w.embed, t["model.embed_tokens.weight"][1])
+    # a norm that is not the identity on rows: a row scaled by 4 maps to the same normalised row
+    t = write_mlx_llama(tmp_path, CFG, seed=7, tie=False, quant_embed=False, embedding_norm="random", files=1)
+    tab = t["model.embed_tokens.weight"][1]
+    tab[1] = (tab[0].astype(np.float32) * 4).astype(np.float16)  # exact: a power of two
+    f = next(tmp_path.glob("*.safetensors"))
+    save_safetensors(f, t)
+    _, w = load_mlx(tmp_path)
+    np.testing.assert_array_equal(w.embed[0], w.embed[1])
+    assert np.abs(w.embed[0].astype(np.float32) - tab[0].astype(np.float32)).max() > 0.05
 
 
 def test_mlx_names_untied_plain_embed(tmp_path):
     t = write_mlx_llama(tmp_path, CFG, seed=2, names="mlx", tie=False, quant_embed=False, sdt="F16", files=3)
     cfg, w = load_mlx(tmp_path, max_seq=40)
     assert cfg.max_seq == 40 and cfg.n_kv_heads == 2
-    np.testing.assert_array_equal(w.embed, t["model.embed_tokens.weight"][1])
+    tab = t["model.embed_tokens.weight"][1].astype(np.float64)
+    en = t["model.embedding_norm.weight"][1].astype(np.float64)
+    rms = np.sqrt(np.linalg.norm(tab, axis=1, keepdims=True) ** 2 / CFG.hidden + CFG.norm_eps)
+    np.testing.assert_allclose(w.embed.astype(np.float64), tab / rms * en, rtol=2 ** -10, atol=1e-4)
     # model.norm is preferred over model.embedding_norm
     np.testing.assert_array_equal(w.final_norm, t["model.norm.weight"][1])
     np.testing.assert_array_equal(w.lm_head[0], _codes(t["lm_head.weight"][1], CFG.vocab))
