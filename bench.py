@@ -345,7 +345,8 @@ def prefill(ctx, engine, n: int, k: int, m: int = 2048, steps: int = 30, warmup:
     if operands != "random":
         out["operands"] = operands
     if affine or x_f32:
-        out["weights"] = "affine u8, scale+bias per 64" if affine else "per-row int8"
+        out["weights"] = ("affine u8, scale+bias per 64, scale table prepared at load (rq_qweight_prepare)"
+                          if affine else "per-row int8")
         out["activations"] = "f32 (cast on device)" if x_f32 else "fp16"
     return out
 
@@ -714,7 +715,8 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "swiglu", "decode", "floor", "vendor", "ops"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "prefill_affine", "swiglu", "decode", "floor", "vendor",
+                                       "ops"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
@@ -746,6 +748,11 @@ def main() -> int:
             out["prefill"] = [prefill(ctx, engine, n, k, steps=args.prefill_steps, use_graph=not args.no_graph,
                                       operands=args.prefill_operands)
                               for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
+        elif args.only == "prefill_affine":
+            # 4096x4096 at M = 2048: per-row codes, then affine codes with fp16 and f32 activations
+            out["prefill"] = [prefill(ctx, engine, 4096, 4096, steps=args.prefill_steps, use_graph=not args.no_graph)]
+            out["prefill_affine"] = [prefill(ctx, engine, 4096, 4096, steps=args.prefill_steps, affine=True, x_f32=f,
+                                             use_graph=not args.no_graph) for f in (False, True)]
         elif args.only == "swiglu":
             out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
         elif args.only == "vendor":
