@@ -797,6 +797,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile("k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>"),
+                     "traffic_profile": "profiles/gemv_decode_m1_4096x4096_pmc.md (FETCH_SIZE + WRITE_SIZE passes, copy-kernel calibrated)",
                      "kernel": "k_gemv_decode<M=1,CPT=1,TPR=256,R=2,ROWWISE>",
                      "mean_launch_us": round(kern_ms * 1e3, 3),
                      "timing": ("device wall clock (rq_device_clock, 100 MHz) stamped on the launch stream "
