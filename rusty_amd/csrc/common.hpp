@@ -129,6 +129,23 @@ int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const voi
 // SwiGLU gate/up pass over RMSNorm(x) . nw (m = 1, f32 x), h fp16.
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
                               float eps, void *h, hipStream_t s);
+// The q/k/v projection of one decode step with its rotary epilogue: the
+// position (device), the (cos, sin) table rope[p * hd/2 + d], the rotated
+// query q (f32 [n_heads][hd]) and this layer's K and V caches
+// [n_kv][max_seq][hd] (fp16), which receive the step's rotated key and value
+// at the position.
+struct RopeDecode {
+    const int *pos = nullptr;
+    const float2 *rope = nullptr;
+    float *q = nullptr;
+    _Float16 *kc = nullptr, *vc = nullptr;
+    int n_heads = 0, n_kv = 0, hd = 0, max_seq = 0;
+};
+// m = 1: [q; k; v] = RMSNorm(x) . nw . W^T (W packed q, k, v rows, head_dim
+// rows per head), then RoPE (rotate-half pairs d, d + hd/2) on q and k; q
+// to rd.q, k and v (fp16) into the caches at *rd.pos.
+int launch_gemv_decode_qkv_rope(const rq_qweight &w, const float *x, const _Float16 *nw, float eps,
+                                const RopeDecode &rd, hipStream_t s);
 // y[n] += sum_k W[n, k] x[k] (m = 1, f32 y) with x the decode attention output
 // combined in the prologue from n_split (1, 2, 4 or 8) partial softmaxes per head
 // of head_dim elements: partials = acc[head][n_split][head_dim] f32, then

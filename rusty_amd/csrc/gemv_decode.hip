@@ -90,6 +90,15 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // split over positions): Xf holds acc[head][SA][attn_hd] (f32) followed by
 // (m, l)[head][SA] (float2); x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
 // M = max_s m_s, rounded to fp16 and shared through LDS like the norm's row.
+// ROPE (with NORM, m = 1): the weight is a Llama layer's packed [q; k; v]
+// (rd.hd rows per head) and the block's local rows come in rotate-half pairs:
+// local rows 2p and 2p + 1 are rows d and d + hd/2 of one head, global pair
+// P = block * ROWS/2 + p covering head P / (hd/2), d = P % (hd/2).  A wave
+// reduces both rows of a pair, so the epilogue rotates them in registers --
+// a = y[d], b = y[d + hd/2]: o[d] = a cos - b sin, o[d + hd/2] = a sin +
+// b cos, angle pos * theta^(-2d/hd) from the table at the step's position
+// (kernels.wgsl:60-79) -- and writes q (f32) to rd.q, k (rotated) and v
+// (fp16) into the caches at that position (rusty-graph/src/lib.rs:235-246).
 // XF (no NORM / SA): the activations are f32 (Xf).  Each 16-value chunk of a
 // row is scaled by a power of two 2^-e that puts its largest magnitude in
 // [2^14, 2^15) (exact), every scaled value is split into two fp16 terms
@@ -97,7 +106,7 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // and the chunk's partial sums are multiplied back by 2^e: any finite f32
 // row is carried without overflowing fp16, and small values keep f32
 // accuracy instead of fp16's subnormal spacing.
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false>
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false, bool ROPE = false>
 __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ W, const float *__restrict__ scales,
                                                     const float *__restrict__ biases,
                                                     const uint8_t *__restrict__ W2, const float *__restrict__ scales2,
@@ -105,20 +114,41 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                                                     const _Float16 *__restrict__ X, const float *__restrict__ Xf,
                                                     const _Float16 *__restrict__ NW, float eps,
                                                     void *__restrict__ Yv, int ymode, int m_act, int N, int K,
-                                                    int group, int attn_hd) {
+                                                    int group, int attn_hd, RopeDecode rd) {
     static_assert(!NORM || M == 1, "the fused norm serves one activation row");
     static_assert(SA == 0 || (M == 1 && !NORM && !SWI), "the attention combine serves one activation row");
     static_assert(!XF || (!NORM && SA == 0), "f32 activations replace the plain fp16 row");
+    static_assert(!ROPE || (NORM && !SWI), "the rotary epilogue serves the normed q/k/v projection");
     constexpr int RP = DT / TPR;
     constexpr int ROWS = R * RP;
     constexpr int TASKS = ROWS * M;
     constexpr int NR = SWI ? 2 * R : R;  // weight rows loaded per row group
+    static_assert(!ROPE || ROWS % 2 == 0, "rotary pairs: an even number of rows per block");
+    constexpr int PAIRS = ROWS / 2;
     __shared__ float part[SWI ? 2 * TASKS : TASKS][TPR];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int rp = t / TPR, tt = t % TPR;
     const int C = K >> 4;
     const int row0 = blockIdx.x * ROWS;
+    // ROPE: the step's position, requested first (the epilogue's table reads
+    // and cache writes depend on it); rotary pairs of this block
+    const int pos = ROPE ? *rd.pos : 0;
+    const int half = ROPE ? rd.hd / 2 : 1;
+    const int pairs_here = ROPE ? min(PAIRS, N / 2 - (int)blockIdx.x * PAIRS) : 0;
+    // ROPE: head and d of the block's first pair (one division per block,
+    // uniform); a block's pairs (PAIRS < hd/2) cross at most one head boundary
+    const int p_first = ROPE ? (int)blockIdx.x * PAIRS : 0;
+    const int head0 = ROPE ? p_first / half : 0, d0 = ROPE ? p_first - head0 * half : 0;
+    // the weight row of local row lr (ROPE: pair lr / 2, row d or d + hd/2 of its head)
+    auto wrow = [&](int lr) -> int {
+        if constexpr (ROPE) {
+            const int dd = d0 + lr / 2, wrap = dd >= half ? 1 : 0;
+            return (head0 + wrap) * rd.hd + (dd - wrap * half) + (lr & 1) * half;
+        } else {
+            return row0 + lr;
+        }
+    };
 
     // X slice (issued first so its wait does not cover the weight stream).
     // NORM: the block loads the f32 row and the norm weight once, spread over
@@ -222,7 +252,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             }
         }
     }
-    const int rows_here = min(ROWS, N - row0);
+    const int rows_here = ROPE ? 2 * pairs_here : min(ROWS, N - row0);  // ROPE: local rows 0 .. 2 pairs_here
     // Per-row scales of the tasks this wave will finish, requested before the
     // weights (and above the prologue's barriers, which the compiler does not
     // move loads across) so the epilogue does not wait on a global load after
@@ -230,7 +260,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     // for its activation row count the weight loads too.
     constexpr int NTW = (TASKS + DT / 64 - 1) / (DT / 64);  // tasks per wave
     float srow[NTW], srow2[SWI ? NTW : 1];
-    if constexpr (FMT == 0) {
+    if constexpr (FMT == 0 && !ROPE) {
 #pragma unroll
         for (int i = 0; i < NTW; ++i) {
             const int rin = (wave + (DT / 64) * i) / M;
@@ -239,12 +269,31 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             if constexpr (SWI) srow2[i] = ok ? scales2[row0 + rin] : 0.0f;
         }
     }
+    // ROPE: wave w finishes pairs w, w + 4, ...: their rows' scales (here)
+    // and the (cos, sin) of their d at the position (after the weight loads:
+    // they wait for the position, which must not hold back the weight stream)
+    constexpr int NPW = (PAIRS + DT / 64 - 1) / (DT / 64);
+    float rs0[ROPE ? NPW : 1], rs1[ROPE ? NPW : 1];
+    float2 rcs[ROPE ? NPW : 1];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            // branch-free: an index past the block's pairs reads row 0's scale, zeroed
+            const int pr = wave + (DT / 64) * i;
+            const bool ok = pr < pairs_here;
+            if constexpr (FMT == 0) {
+                const float a = scales[ok ? wrow(2 * pr) : 0], b = scales[ok ? wrow(2 * pr + 1) : 0];
+                rs0[i] = ok ? a : 0.0f;
+                rs1[i] = ok ? b : 0.0f;
+            }
+        }
+    }
     // y += result: the old values of the residual, requested now for the same reason
     float yold[NTW];
 #pragma unroll
     for (int i = 0; i < NTW; ++i) {
         const int task = wave + (DT / 64) * i, rin = task / M, m = task % M;
-        yold[i] = (ymode == kYAdd && task < TASKS && rin < rows_here && m < m_act)
+        yold[i] = (!ROPE && ymode == kYAdd && task < TASKS && rin < rows_here && m < m_act)
                       ? reinterpret_cast<const float *>(Yv)[(size_t)m * N + row0 + rin]
                       : 0.0f;
     }
@@ -266,25 +315,36 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                 // for the previous): a chunk past K multiplies zero activations
                 // and a row past N is not stored, so those take group 0's values
                 const int c = tt + TPR * j;
-                const size_t g = c < C && rin < rows_here ? (size_t)(row0 + rin) * gk + cg[j] : 0;
+                const size_t g = c < C && rin < rows_here ? (size_t)wrow(rin) * gk + cg[j] : 0;
                 sg[r][j] = sp[g];
                 bg[r][j] = bp ? bp[g] : 0.0f;
             }
         }
     }
 
-    // Weight chunks: R rows x CPT chunks per thread, all in flight.
-    const auto rw = make_rsrc(W + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
+    // Weight chunks: R rows x CPT chunks per thread, all in flight.  ROPE:
+    // one resource over the whole weight, rows by the pair mapping.
+    const auto rw = ROPE ? make_rsrc(W, (uint32_t)N * (uint32_t)K)
+                         : make_rsrc(W + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
     const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)row0 * K, (uint32_t)rows_here * (uint32_t)K);
     uint4 w[NR][CPT];
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            const int c = tt + TPR * j;
-            const uint32_t off = c < C ? (uint32_t)((r % R) * RP + rp) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
+            const int c = tt + TPR * j, lr = (r % R) * RP + rp;
+            uint32_t off = c < C ? (uint32_t)lr * (uint32_t)K + (uint32_t)c * 16 : kOOB;
+            if constexpr (ROPE) off = c < C && lr < rows_here ? (uint32_t)wrow(lr) * (uint32_t)K + (uint32_t)c * 16 : kOOB;
             w[r][j] = bload<2>(r < R ? rw : rw2, off);
         }
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            const int pr = wave + (DT / 64) * i;
+            const int dd = d0 + pr, d = dd >= half ? dd - half : dd;
+            rcs[i] = rd.rope[(size_t)pos * half + (pr < pairs_here ? d : 0)];
+        }
+    }
     if constexpr (SA > 0) {
         __shared__ uint4 xsa[XC * 2];  // the combined fp16 row, 2 x 16 B per chunk
 #pragma unroll
@@ -462,6 +522,43 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     }
     __syncthreads();
 
+    if constexpr (ROPE) {
+        // Each wave finishes whole rotary pairs: both rows' sums, the rotation,
+        // the stores (q f32; k and v fp16 into the caches at the position).
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            const int pr = wave + (DT / 64) * i;
+            if (pr >= PAIRS) break;
+            float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < TPR / 64; ++u) {
+                v0 += part[2 * pr][lane + 64 * u];
+                v1 += part[2 * pr + 1][lane + 64 * u];
+            }
+            const float a0 = wave_total(v0), a1 = wave_total(v1);
+            if (lane == 0 && pr < pairs_here) {
+                const float y0 = FMT == 0 ? a0 * rs0[i] : a0, y1 = FMT == 0 ? a1 * rs1[i] : a1;
+                const int dd = d0 + pr, wrap = dd >= half ? 1 : 0;
+                const int head = head0 + wrap, d = dd - wrap * half;
+                const float c = rcs[i].x, sn = rcs[i].y;
+                if (head < rd.n_heads) {
+                    float *qh = rd.q + (size_t)head * rd.hd;
+                    qh[d] = y0 * c - y1 * sn;
+                    qh[d + half] = y0 * sn + y1 * c;
+                } else if (head < rd.n_heads + rd.n_kv) {
+                    _Float16 *kh = rd.kc + ((size_t)(head - rd.n_heads) * rd.max_seq + pos) * rd.hd;
+                    kh[d] = (_Float16)(y0 * c - y1 * sn);
+                    kh[d + half] = (_Float16)(y0 * sn + y1 * c);
+                } else {
+                    _Float16 *vh = rd.vc + ((size_t)(head - rd.n_heads - rd.n_kv) * rd.max_seq + pos) * rd.hd;
+                    vh[d] = (_Float16)y0;
+                    vh[d + half] = (_Float16)y1;
+                }
+            }
+        }
+        return;
+    }
+
     // Each wave finishes whole (row, token) tasks.
 #pragma unroll
     for (int i_t = 0; i_t < NTW; ++i_t) {
@@ -491,7 +588,7 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
 
 using DecodeFn = void (*)(const uint8_t *, const float *, const float *, const uint8_t *, const float *,
                           const float *, const _Float16 *, const float *, const _Float16 *, float, void *, int, int, int, int, int,
-                          int);
+                          int, RopeDecode);
 
 // A kernel instance and the rows per row group (R) it was compiled for; the
 // grid is derived from the same R.
@@ -499,8 +596,8 @@ struct Decode {
     DecodeFn fn;
     int r;
 };
-template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false>
-constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM, SA, XF>, R}; }
+template <int M, int CPT, int TPR, int R, int FMT, bool SWI, bool NORM, int SA = 0, bool XF = false, bool ROPE = false>
+constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM, SA, XF, ROPE>, R}; }
 
 // Rows per row group, measured on MI355X with the weights streamed from HBM:
 //  m = 1:
@@ -522,11 +619,12 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 // pass; norm (m = 1) the fused RMSNorm prologue; sa (m = 1) the attention
 // combine of sa partials per head; xf (m <= 2, no norm / sa) f32 activations.
 template <int M, int CPT, int TPR, int FMT>
-Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf) {
+Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
     if constexpr (M == 1) {
         constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
         constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
         constexpr int RP = FMT == 0 && CPT >= 2 ? 4 : 2;
+        if (rope) return inst<1, CPT, TPR, RN, FMT, false, true, 0, false, true>();
         if (sa == 1) return inst<1, CPT, TPR, 4, FMT, false, false, 1>();
         if (sa == 2) return inst<1, CPT, TPR, 4, FMT, false, false, 2>();
         if (sa == 4) return inst<1, CPT, TPR, 4, FMT, false, false, 4>();
@@ -545,6 +643,7 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf) {
         (void)norm;
         (void)tall;
         (void)sa;
+        (void)rope;
         if (swi) return xf ? inst<2, CPT, TPR, 2, FMT, true, false, 0, true>() : inst<2, CPT, TPR, 2, FMT, true, false>();
         return xf ? inst<2, CPT, TPR, 4, FMT, false, false, 0, true>() : inst<2, CPT, TPR, 4, FMT, false, false>();
     } else {
@@ -552,33 +651,34 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf) {
         (void)tall;
         (void)sa;
         (void)xf;
+        (void)rope;
         if (swi) return inst<M, CPT, TPR, 2, FMT, true, false>();
         return inst<M, CPT, TPR, 4, FMT, false, false>();
     }
 }
 
 template <int M, int CPT, int TPR>
-Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
-    return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa, xf)
-                    : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa, xf);
+Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
+    return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa, xf, rope)
+                    : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa, xf, rope);
 }
 
 template <int M, int CPT>
-Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
+Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
     switch (tpr) {
-    case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa, xf);
-    case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa, xf);
-    default: return pick_swi<M, CPT, 256>(fmt, swi, norm, tall, sa, xf);
+    case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa, xf, rope);
+    case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa, xf, rope);
+    default: return pick_swi<M, CPT, 256>(fmt, swi, norm, tall, sa, xf, rope);
     }
 }
 
 template <int M>
-Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
     switch (cpt) {
-    case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa, xf);
-    case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa, xf);
-    case 3: return pick_tpr<M, 3>(tpr, fmt, swi, norm, tall, sa, xf);
-    default: return pick_tpr<M, 4>(tpr, fmt, swi, norm, tall, sa, xf);
+    case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa, xf, rope);
+    case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa, xf, rope);
+    case 3: return pick_tpr<M, 3>(tpr, fmt, swi, norm, tall, sa, xf, rope);
+    default: return pick_tpr<M, 4>(tpr, fmt, swi, norm, tall, sa, xf, rope);
     }
 }
 
@@ -586,7 +686,7 @@ Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int s
 
 // The kernel instance for a supported call and the weight rows each of its
 // blocks covers (block j: rows j * rows ..).
-static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool xf, int *rows) {
+static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool xf, bool rope, int *rows) {
     const int64_t N = w.n_out, K = w.k_in;
     const int C = (int)(K / 16);
     const int tpr = C <= 64 ? 64 : (C <= 128 ? 128 : 256);
@@ -594,9 +694,9 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
     const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
     const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall, sa, xf)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xf)
-                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0, false);
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall && !rope, sa, xf, rope)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xf, false)
+                                       : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0, false, false);
     *rows = d.r * (DT / tpr);
     return d;
 }
@@ -605,7 +705,8 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool
 // with the fp16 weight nw and epsilon eps, or (sa > 0, m = 1) the attention
 // partials to combine (sa per head of attn_hd elements).
 static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *x, const _Float16 *nw, float eps,
-                         void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0, bool xf = false) {
+                         void *y, int ymode, int m, hipStream_t s, int sa = 0, int attn_hd = 0, bool xf = false,
+                         const RopeDecode *rd = nullptr) {
     const int64_t N = w.n_out, K = w.k_in;
     // f32 activations: m <= 2 and the plain row only; 32-bit offsets into X
     if (xf && (m > 2 || nw || sa || (int64_t)m * K * 4 > 0x7fffffffll)) return RQ_ERR_UNSUPPORTED;
@@ -618,14 +719,21 @@ static int launch_decode(const rq_qweight &w, const rq_qweight *w2, const void *
     if (sa && (m != 1 || w2 || nw || (sa != 1 && sa != 2 && sa != 4 && sa != 8) || attn_hd < 8 ||
                attn_hd % 8 != 0 || K % attn_hd != 0))
         return RQ_ERR_UNSUPPORTED;
+    // the rotary epilogue: the normed m = 1 projection of whole heads, the
+    // whole weight addressable with 32-bit offsets
+    // (hd >= 32: a block's pairs, at most 12, cross at most one head boundary)
+    if (rd && (!nw || m != 1 || w2 || sa || xf || rd->hd < 32 || rd->hd % 2 != 0 ||
+               N != (int64_t)(rd->n_heads + 2 * rd->n_kv) * rd->hd || N * K > 0xffffffffll || !rd->pos ||
+               !rd->rope || !rd->q || !rd->kc || !rd->vc))
+        return RQ_ERR_UNSUPPORTED;
     int rows;
-    const Decode d = plan(w, w2 != nullptr, nw != nullptr, m, sa, xf, &rows);
+    const Decode d = plan(w, w2 != nullptr, nw != nullptr, m, sa, xf, rd != nullptr, &rows);
     const bool fx = nw || sa || xf;  // x is an f32 source
     const int64_t blocks = cdiv(N, rows);
     hipLaunchKernelGGL(d.fn, dim3((unsigned)blocks), dim3(DT), 0, s, (const uint8_t *)w.codes, w.scales, w.biases,
                        w2 ? (const uint8_t *)w2->codes : nullptr, w2 ? w2->scales : nullptr, w2 ? w2->biases : nullptr,
                        fx ? nullptr : (const _Float16 *)x, fx ? (const float *)x : nullptr, nw, eps, y, ymode, m,
-                       (int)N, (int)K, w.group, attn_hd);
+                       (int)N, (int)K, w.group, attn_hd, rd ? *rd : RopeDecode{});
     RQ_LAUNCH_CHECK();
     return RQ_OK;
 }
@@ -651,6 +759,11 @@ int launch_swiglu_decode(const rq_qweight &gate, const rq_qweight &up, const voi
 int launch_swiglu_decode_norm(const rq_qweight &gate, const rq_qweight &up, const float *x, const _Float16 *nw,
                               float eps, void *h, hipStream_t s) {
     return launch_decode(gate, &up, x, nw, eps, h, kYF16, 1, s);
+}
+
+int launch_gemv_decode_qkv_rope(const rq_qweight &w, const float *x, const _Float16 *nw, float eps,
+                                const RopeDecode &rd, hipStream_t s) {
+    return launch_decode(w, nullptr, x, nw, eps, nullptr, kYF32, 1, s, 0, 0, false, &rd);
 }
 
 int launch_gemv_decode_attn_add(const rq_qweight &w, const float *partials, int n_split, int head_dim, float *y,

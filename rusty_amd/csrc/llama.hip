@@ -5,10 +5,12 @@
 // Per block (LlamaBlock::forward, rusty-graph/src/lib.rs:364-378):
 //   qkv  = rmsnorm(x, attn_norm) . [Wq;Wk;Wv]^T   decode GEMV with the RMSNorm
 //                                                 in its prologue (q, k, v
-//                                                 packed into one weight)
-//   attn = softmax(rope(q) . K^T / sqrt(d)) . V   k_attn_decode (RoPE, KV
-//                                                 append, GQA attention, split
-//                                                 over positions: partials)
+//                                                 packed into one weight), RoPE
+//                                                 and the KV append in its
+//                                                 epilogue
+//   attn = softmax(q . K^T / sqrt(d)) . V         k_attn_decode (GQA attention
+//                                                 over the cache, split over
+//                                                 positions: partials)
 //   x   += attn . Wo^T                            decode GEMV: the partials are
 //                                                 combined in its prologue, add
 //                                                 epilogue
@@ -128,133 +130,107 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
     }
 }
 
-// Decode attention at position pos = *pos_p, split over positions: block
-// (head hd, split sp) of a grid of n_heads * S covers positions [r0, r1) of
-// 0..pos, P = ceil((pos + 1) / S) positions per split, and writes its partial
-// softmax -- the running max m, the sum l of exp(score - m) and the
-// unnormalised accumulator acc[d] = sum exp(score - m) * v[d] -- to
-// part[(hd * S + sp) * HD + d] and ml[hd * S + sp] = (m, l).  An empty range
-// (pos + 1 < S) writes (-inf, 0, 0).  The consumer (the o-projection GEMV's
-// prologue) combines the S partials of a head: out = sum_s e^(m_s - M) acc_s /
-// sum_s e^(m_s - M) l_s, M = max_s m_s.
+// Decode attention at position pos = *pos_p, split over positions in tiles
+// of one pass (PASS positions): block (head hd, split sp) of a grid of
+// n_heads * S takes tiles sp, sp + S, sp + 2 S, ... of positions 0..pos and
+// writes its partial softmax -- the running max m, the sum l of
+// exp(score - m) and the unnormalised accumulator acc[d] = sum exp(score - m)
+// * v[d] -- to part[(hd * S + sp) * HD + d] and ml[hd * S + sp] = (m, l).  A
+// block with no position (sp * PASS > pos) writes (-inf, 0, 0).  The
+// consumer (the o-projection GEMV's prologue) combines the S partials of a
+// head: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s, M = max_s m_s.
 //
-// RoPE (kernels.wgsl:60-79, rotate-half pairs (d, d + HD/2), angle
-// pos * theta^(-2d/HD) from a (cos, sin) table built once at create) is
-// applied to q and to the new key; the block that holds position pos in the
-// first query head of each KV group appends the new key and value (rounded
-// to fp16) to the cache at `pos` (rusty-graph/src/lib.rs:235-246).  Every
-// block uses the new key/value from LDS for position pos and reads the cache
-// only below pos (the buffer resource ends there; rows past it read as zero),
-// so no block reads what another block of this launch writes.  Scores
-// q.k / sqrt(HD), softmax in f32.  GQA: query head h reads KV head
+// The q/k/v projection before it (launch_gemv_decode_qkv_rope) has already
+// rotated q and k (RoPE, kernels.wgsl:60-79) and appended this position's
+// key and value to the cache (rusty-graph/src/lib.rs:235-246), so the block
+// reads only the rotated query (f32) and cache rows 0..pos.  Its first tile
+// does not depend on the position, so the position, the query and that
+// tile's K/V rows are requested together at the start: one memory round trip
+// before the arithmetic (cache rows past pos are loaded -- whatever an
+// earlier sequence left there -- and zeroed once the position is known).
+// Scores q.k / sqrt(HD), softmax in f32.  GQA: query head h reads KV head
 // h / (n_heads / n_kv) (flash_attention_v2.wgsl:79-83).
 //
-// Latency-bound: each block streams its range's K and V rows (2 * P * HD * 2
-// bytes) through one CU, so splitting a head's context over S blocks divides
-// that stream; the first pass's rows are requested right after pos is read,
-// before the RoPE prologue.  A pass covers 8 waves x RW consecutive rows
-// each; lane l holds 16-byte chunk l % CH of row i * RPI + l / CH for i < NI,
-// all in flight before any is used.  The block's work is a serial chain of
-// short dependent steps, so it is spread thin: 8 waves of 4 row loads
-// measured 1.4-1.6 % more tokens/s for the whole decode step than 4 waves of
-// 8 (16 waves of 2: +0.7 %), and 8 waves of 2 another 1.0 % (an 80-row
-// split then keeps 5 waves busy instead of 3; 8 waves of 1 load, two passes
-// per split: -1.0 %).  Row scores finish with DPP steps over the CH
-// lanes of a row; P.V partials are summed over the lanes of a chunk, then over
-// waves in LDS; passes beyond the first combine by the online-softmax rescale.
+// Latency-bound: each block streams its tiles' K and V rows through one CU,
+// so splitting a head's context over S blocks divides that stream.  A pass
+// covers 8 waves x RW consecutive rows each; lane l holds 16-byte chunk
+// l % CH of row i * RPI + l / CH for i < NI, all in flight before any is
+// used.  The block's work is a serial chain of short dependent steps, so it
+// is spread thin: 8 waves of 4 row loads measured 1.4-1.6 % more tokens/s
+// for the whole decode step than 4 waves of 8 (16 waves of 2: +0.7 %), and 8
+// waves of 2 another 1.0 %.  Row scores finish with DPP steps over the CH
+// lanes of a row; P.V partials are summed over the lanes of a chunk, then
+// over waves in LDS; tiles beyond the first combine by the online-softmax
+// rescale.
 constexpr int ATT = 512;  // threads per attention block
 
 template <int HD>
-__global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ qkv, _Float16 *__restrict__ kc,
-                                                     _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
-                                                     const float2 *__restrict__ rope, float *__restrict__ part,
-                                                     float2 *__restrict__ ml, int n_heads, int n_kv, int max_seq,
-                                                     int S) {
+__global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q, const _Float16 *__restrict__ kc,
+                                                     const _Float16 *__restrict__ vc, const int *__restrict__ pos_p,
+                                                     float *__restrict__ part, float2 *__restrict__ ml, int n_heads,
+                                                     int n_kv, int max_seq, int S) {
     constexpr int NW = ATT / 64;
     constexpr int CH = HD / 8;         // 16-byte chunks per row
     constexpr int RPI = 64 / CH;       // rows per wave-wide load
     constexpr int NI = 2;              // loads of K (and of V) per lane per pass
     constexpr int RW = NI * RPI;       // rows per wave per pass
-    constexpr int PASS = NW * RW;      // positions per pass
-    constexpr int HALF = HD / 2;
-    __shared__ float qs[HD], kn[HD], vn[HD], redm[NW], reds[NW];
+    constexpr int PASS = NW * RW;      // positions per pass (one tile)
+    __shared__ float redm[NW], reds[NW];
     __shared__ float accs[NW][4][HD];
     const int hd = blockIdx.x / S, sp = blockIdx.x % S, t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int pos = *pos_p;
-    const int T = pos + 1, P = (T + S - 1) / S;
-    const int r0 = min(T, sp * P), r1 = min(T, r0 + P);  // this block's positions [r0, r1)
     const int grp = n_heads / n_kv, g = hd / grp;
-    _Float16 *kcg = kc + (size_t)g * max_seq * HD;
-    _Float16 *vcg = vc + (size_t)g * max_seq * HD;
-    const auto rk = make_rsrc(kcg, (uint32_t)pos * HD * 2u);
-    const auto rv = make_rsrc(vcg, (uint32_t)pos * HD * 2u);
+    // the whole cache of this KV head: rows up to max_seq (past it: zeros)
+    const auto rk = make_rsrc(kc + (size_t)g * max_seq * HD, (uint32_t)max_seq * HD * 2u);
+    const auto rv = make_rsrc(vc + (size_t)g * max_seq * HD, (uint32_t)max_seq * HD * 2u);
     const int ch = lane % CH, rl = lane / CH;
     uint4 kr[NI], vr[NI];
-    auto load_pass = [&](int c0) {
+    auto load_tile = [&](int c0) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int row = c0 + RW * w + i * RPI + rl;
-            const uint32_t off = row < r1 && row < pos ? ((uint32_t)row * HD + (uint32_t)ch * 8) * 2u : kOOB;
-            kr[i] = bload(rk, off);
-            vr[i] = bload(rv, off);
+            const uint32_t row = (uint32_t)(c0 + RW * w + i * RPI + rl);
+            const uint32_t off = ((row * HD + (uint32_t)ch * 8) * 2u);
+            kr[i] = bload(rk, row < (uint32_t)max_seq ? off : kOOB);
+            vr[i] = bload(rv, row < (uint32_t)max_seq ? off : kOOB);
         }
     };
-    load_pass(r0);
-
-    const float *q = qkv + (size_t)hd * HD;
-    const float *k = qkv + (size_t)n_heads * HD + (size_t)g * HD;
-    const float *v = qkv + (size_t)(n_heads + n_kv) * HD + (size_t)g * HD;
-    // this position's q, k, v and RoPE factors, all requested before any is
-    // used (one round trip: a separate branch for v waited for the others
-    // first, a second round trip on the block's critical path)
-    if (t < HD) {
-        const int d = t % HALF;
-        const float2 cs = rope[(size_t)pos * HALF + d];  // (cos, sin) of pos * theta^(-2d/HD)
-        const float q1 = q[d], q2 = q[d + HALF], k1 = k[d], k2 = k[d + HALF], vv = v[t];
-        if (t < HALF) {
-            qs[t] = q1 * cs.x - q2 * cs.y;
-            qs[t + HALF] = q1 * cs.y + q2 * cs.x;
-            kn[t] = (float)(_Float16)(k1 * cs.x - k2 * cs.y);
-            kn[t + HALF] = (float)(_Float16)(k1 * cs.y + k2 * cs.x);
-        }
-        vn[t] = (float)(_Float16)vv;
-    }
-    __syncthreads();
-    if (hd % grp == 0 && r1 == T && r0 < r1 && t < HD) {
-        kcg[(size_t)pos * HD + t] = (_Float16)kn[t];
-        vcg[(size_t)pos * HD + t] = (_Float16)vn[t];
-    }
+    const int c_first = sp * PASS;
+    load_tile(c_first);  // before the position is known
+    const int pos = *pos_p;
+    // this lane's 8 elements of the rotated query
     float qv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[e] = qs[ch * 8 + e];
-    // score of the new key (position pos), reduced over the CH lanes of a row
-    float s_new = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s_new = fmaf(qv[e], kn[ch * 8 + e], s_new);
-    s_new = group_sum<CH>(s_new);
+    {
+        const float4 *qp = reinterpret_cast<const float4 *>(q + (size_t)hd * HD + ch * 8);
+        const float4 a = qp[0], b = qp[1];
+        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w;
+        qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+    }
+    const int T = pos + 1;
 
     const float scale = 1.0f / sqrtf((float)HD);
     float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int c0 = r0; c0 < r1; c0 += PASS) {
+    for (int c0 = c_first; c0 < T; c0 += S * PASS) {
         const int base = c0 + RW * w;
-        if (c0 > r0) load_pass(c0);  // the first pass was requested before the prologue
-        const bool live = base < r1;  // wave-uniform: waves past the range only join the reductions
+        if (c0 > c_first) load_tile(c0);  // the first tile was requested at the start
+        const bool live = base < T;  // wave-uniform: waves past the position only join the reductions
         float sv[NI];
         float lm = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             sv[i] = -__builtin_inff();
+            const int row = base + i * RPI + rl;
+            if (row >= T) {  // a row past the position: not this sequence's (yet)
+                kr[i] = make_uint4(0, 0, 0, 0);
+                vr[i] = make_uint4(0, 0, 0, 0);
+            }
             if (!live) continue;
             float f[8], sc = 0.0f;
             widen8(kr[i], f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) sc = fmaf(qv[e], f[e], sc);
             sc = group_sum<CH>(sc);
-            const int row = base + i * RPI + rl;
-            sc = row == pos ? s_new : sc;
-            sv[i] = row < r1 ? sc * scale : -__builtin_inff();
+            sv[i] = row < T ? sc * scale : -__builtin_inff();
             lm = fmaxf(lm, sv[i]);
         }
         lm = wave_max(lm);
@@ -263,7 +239,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
         float cm = redm[0];
 #pragma unroll
         for (int i = 1; i < NW; ++i) cm = fmaxf(cm, redm[i]);
-        const float m_new = fmaxf(m_run, cm);  // finite: row r0 is in the first pass
+        const float m_new = fmaxf(m_run, cm);  // finite: row c0 (< T) is in every tile the loop visits
         const float alpha = expf(m_run - m_new);
         float ls = 0.0f;
 #pragma unroll
@@ -271,16 +247,11 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             if (!live) break;
-            const float p = expf(sv[i] - m_new);
-            const int row = base + i * RPI + rl;
+            const float p = expf(sv[i] - m_new);  // 0 for rows past the position (their V is zeroed)
             float f[8];
-            widen8(vr[i], f);  // rows at pos and past the range read as zero
+            widen8(vr[i], f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, f[e], acc[e]);
-            if (row == pos) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, vn[ch * 8 + e], acc[e]);
-            }
             ls += ch == 0 ? p : 0.0f;  // one lane per row counts it
         }
         ls = wave_sum(ls);
@@ -291,7 +262,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
         for (int i = 0; i < NW; ++i) cl += reds[i];
         l_run = l_run * alpha + cl;
         m_run = m_new;
-        __syncthreads();  // redm / reds are rewritten by the next pass
+        __syncthreads();  // redm / reds are rewritten by the next tile
     }
     // sum P.V partials over the lanes holding the same chunk: within a 16-lane
     // row (HD = 64: two rows of 8 chunks, row_ror 8 pairs lane i with i + 8),
@@ -447,18 +418,28 @@ int enqueue_step(rq_llama *md, hipStream_t s) {
     int st;
     for (int l = 0; l < c.n_layers; ++l) {
         const rq_llama::Layer &L = md->layers[l];
-        if ((st = launch_gemv_decode_norm(L.qkv, md->x, L.attn_norm, c.norm_eps, md->qkv_out, s)) != RQ_OK)
-            return st;
+        // q/k/v with RoPE and the KV append in the projection's epilogue
+        RopeDecode rd;
+        rd.pos = md->pos;
+        rd.rope = md->rope;
+        rd.q = md->qkv_out;  // rotated q: the first n_heads * head_dim values
+        rd.kc = md->kc + l * kv_layer;
+        rd.vc = md->vc + l * kv_layer;
+        rd.n_heads = c.n_heads;
+        rd.n_kv = c.n_kv_heads;
+        rd.hd = c.head_dim;
+        rd.max_seq = c.max_seq;
+        if ((st = launch_gemv_decode_qkv_rope(L.qkv, md->x, L.attn_norm, c.norm_eps, rd, s)) != RQ_OK) return st;
         const int S = md->n_split;
         float2 *ml = reinterpret_cast<float2 *>(md->part + (size_t)c.n_heads * S * c.head_dim);
         if (c.head_dim == 64)
             hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads * S), dim3(ATT), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->part, ml,
-                               c.n_heads, c.n_kv_heads, c.max_seq, S);
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->part, ml, c.n_heads,
+                               c.n_kv_heads, c.max_seq, S);
         else
             hipLaunchKernelGGL(k_attn_decode<128>, dim3(c.n_heads * S), dim3(ATT), 0, s, md->qkv_out,
-                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->rope, md->part, ml,
-                               c.n_heads, c.n_kv_heads, c.max_seq, S);
+                               md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->part, ml, c.n_heads,
+                               c.n_kv_heads, c.max_seq, S);
         RQ_LAUNCH_CHECK();
         if ((st = launch_gemv_decode_attn_add(L.o, md->part, S, c.head_dim, md->x, s)) != RQ_OK) return st;
         if ((st = launch_swiglu_decode_norm(L.gate, L.up, md->x, L.mlp_norm, c.norm_eps, md->h, s)) != RQ_OK)
@@ -704,11 +685,13 @@ int rq_llama_create(rq_ctx *ctx, const rq_llama_config *cfg, const rq_llama_weig
         bytes += pad(affine_prep_bytes(qkv_of(l))) + pad(table_bytes(src.o)) + pad(table_bytes(src.gate)) +
                  pad(table_bytes(src.up)) + pad(table_bytes(src.down));
     }
-    // attention splits: ~160 positions of the cache per block up to 480 (each
-    // block's K/V rows stream through one CU), 8 beyond (for 640 positions 8
-    // splits measured 1.7 % more tokens/s than 4, with the o-projection
-    // re-reading twice the partials in every block)
-    const int n_split = c.max_seq <= 160 ? 1 : (c.max_seq <= 320 ? 2 : (c.max_seq <= 480 ? 4 : 8));
+    // attention splits: enough blocks per head that a full cache is one tile
+    // (one pass: 128 positions at head_dim 64, 64 at 128) per block, the
+    // count a power of two up to 8 (the o-projection's combine serves 1, 2, 4
+    // and 8); longer caches give each block several tiles
+    const int pass_rows = c.head_dim == 64 ? 128 : 64;
+    const int tiles = (int)cdiv(c.max_seq, pass_rows);
+    const int n_split = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : (tiles <= 4 ? 4 : 8));
     const size_t part_floats = (size_t)c.n_heads * n_split * (c.head_dim + 2);
     bytes += pad(H * 4) + pad(QKV * 4) + pad((size_t)c.vocab * 4) + pad(part_floats * 4) + pad(2 * I * 2) +
              2 * pad(kv * 2) + pad(((size_t)c.max_seq + 1) * 4) + 2 * pad(4) +

@@ -245,9 +245,9 @@ class LlamaRunner:
             self._keep.append(t)
             return t.ptr
 
-        def dev_q(lin):
+        def dev_q(lin, prepare=True):
             qt = QuantizedTensor.rowwise(ctx, *lin) if len(lin) == 2 else QuantizedTensor.affine(
-                ctx, lin[0], lin[1], lin[2], group=lin[3])
+                ctx, lin[0], lin[1], lin[2], group=lin[3], prepare=prepare)
             self._keep.append(qt)
             return qt.descriptor()
 
@@ -256,8 +256,10 @@ class LlamaRunner:
             L = layers[i]
             L.attn_norm = dev_f16(lw["attn_norm"])
             L.mlp_norm = dev_f16(lw["mlp_norm"])
+            # q, k and v are packed into one weight by the runner, which builds
+            # that weight's prefill scale table itself
             for name in ("q", "k", "v", "o", "gate", "up", "down"):
-                setattr(L, name, dev_q(lw[name]))
+                setattr(L, name, dev_q(lw[name], prepare=name not in ("q", "k", "v")))
         self._layers = layers
         cw = rq_llama_weights(dev_f16(weights.embed), layers, dev_f16(weights.final_norm), dev_q(weights.lm_head))
         self._cfg = cfg.c_struct()
