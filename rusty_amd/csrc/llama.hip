@@ -159,9 +159,10 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
 // is spread thin: 8 waves of 4 row loads measured 1.4-1.6 % more tokens/s
 // for the whole decode step than 4 waves of 8 (16 waves of 2: +0.7 %), and 8
 // waves of 2 another 1.0 %.  Row scores finish with DPP steps over the CH
-// lanes of a row; P.V partials are summed over the lanes of a chunk, then
-// over waves in LDS; tiles beyond the first combine by the online-softmax
-// rescale.
+// lanes of a row; each wave runs its own online softmax (max and sum by DPP
+// steps and readlanes, tiles beyond the first by the rescale), and the P.V
+// partials are summed over the lanes of a chunk, then over waves in LDS
+// weighted by e^(m_w - M): one barrier per block.
 constexpr int ATT = 512;  // threads per attention block
 
 template <int HD>
@@ -206,6 +207,9 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     }
     const int T = pos + 1;
 
+    // Each wave keeps its own online softmax over its rows of every tile
+    // (running max m, sum l, accumulator acc): no barrier inside the loop.
+    // The block's waves merge once at the end.
     const float scale = 1.0f / sqrtf((float)HD);
     float m_run = -__builtin_inff(), l_run = 0.0f, acc[8];
 #pragma unroll
@@ -213,18 +217,16 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     for (int c0 = c_first; c0 < T; c0 += S * PASS) {
         const int base = c0 + RW * w;
         if (c0 > c_first) load_tile(c0);  // the first tile was requested at the start
-        const bool live = base < T;  // wave-uniform: waves past the position only join the reductions
+        if (base >= T) break;  // wave-uniform: this wave's rows of this and later tiles are past the position
         float sv[NI];
         float lm = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            sv[i] = -__builtin_inff();
             const int row = base + i * RPI + rl;
             if (row >= T) {  // a row past the position: not this sequence's (yet)
                 kr[i] = make_uint4(0, 0, 0, 0);
                 vr[i] = make_uint4(0, 0, 0, 0);
             }
-            if (!live) continue;
             float f[8], sc = 0.0f;
             widen8(kr[i], f);
 #pragma unroll
@@ -233,20 +235,14 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
             sv[i] = row < T ? sc * scale : -__builtin_inff();
             lm = fmaxf(lm, sv[i]);
         }
-        lm = wave_max(lm);
-        if (lane == 0) redm[w] = lm;
-        __syncthreads();
-        float cm = redm[0];
-#pragma unroll
-        for (int i = 1; i < NW; ++i) cm = fmaxf(cm, redm[i]);
-        const float m_new = fmaxf(m_run, cm);  // finite: row c0 (< T) is in every tile the loop visits
+        // finite: the wave's first row (base < T) is live
+        const float m_new = fmaxf(m_run, wave_max(lm));
         const float alpha = expf(m_run - m_new);
         float ls = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            if (!live) break;
             const float p = expf(sv[i] - m_new);  // 0 for rows past the position (their V is zeroed)
             float f[8];
             widen8(vr[i], f);
@@ -254,19 +250,13 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
             for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, f[e], acc[e]);
             ls += ch == 0 ? p : 0.0f;  // one lane per row counts it
         }
-        ls = wave_sum(ls);
-        if (lane == 0) reds[w] = ls;
-        __syncthreads();
-        float cl = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) cl += reds[i];
-        l_run = l_run * alpha + cl;
+        l_run = l_run * alpha + wave_sum(ls);
         m_run = m_new;
-        __syncthreads();  // redm / reds are rewritten by the next tile
     }
     // sum P.V partials over the lanes holding the same chunk: within a 16-lane
     // row (HD = 64: two rows of 8 chunks, row_ror 8 pairs lane i with i + 8),
-    // then over the four rows of each wave and over waves in LDS
+    // then over the four rows of each wave and over waves in LDS, each wave's
+    // sums weighted by e^(m_w - M), M the block's max
     if constexpr (CH == 8) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] += dpp<0x128>(acc[e]);
@@ -275,17 +265,31 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
 #pragma unroll
         for (int e = 0; e < 8; ++e) accs[w][lane >> 4][ch * 8 + e] = acc[e];
     }
+    if (lane == 0) {
+        redm[w] = m_run;
+        reds[w] = l_run;
+    }
     __syncthreads();
     const size_t slot = (size_t)hd * S + sp;
     if (t < HD) {
-        float sum = 0.0f;
+        float M = redm[0];
 #pragma unroll
-        for (int i = 0; i < NW; ++i)
+        for (int i = 1; i < NW; ++i) M = fmaxf(M, redm[i]);
+        float sum = 0.0f, L = 0.0f;
+        if (M != -__builtin_inff()) {  // else: no position in this block's tiles
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sum += accs[i][j][t];
+            for (int i = 0; i < NW; ++i) {
+                const float f = expf(redm[i] - M);  // 0 for a wave with no row
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a += accs[i][j][t];
+                sum = fmaf(f, a, sum);
+                L = fmaf(f, reds[i], L);
+            }
+        }
         part[slot * HD + t] = sum;
+        if (t == 0) ml[slot] = make_float2(M, L);
     }
-    if (t == 0) ml[slot] = make_float2(m_run, l_run);
 }
 
 constexpr int AT = 1024;
