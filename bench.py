@@ -545,6 +545,29 @@ def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eag
                                 "stepwise: the same prompt one position at a time through the step graph"}}
 
 
+def decode_probe(ctx, prompt_len: int = 512, steps: int = 8) -> dict:
+    """The configs[4] runner's kernels for counter passes: the bench's 512-token
+    prompt through the batched prefill, then `steps` single decode steps as
+    direct launches, one progress line per step (a counter pass serialises
+    every dispatch; the full decode loop's ~100k are too slow for that)."""
+    from rusty_amd.llama import LLAMA_1B, LlamaRunner, synth_weights
+
+    cfg = LLAMA_1B
+    runner = LlamaRunner(ctx, cfg, synth_weights(cfg, seed=0))
+    runner.set_graph(False)
+    log("decode probe: runner created")
+    runner.prefill(np.random.default_rng(1).integers(0, cfg.vocab, prompt_len))
+    runner.tokens()
+    log("decode probe: prefill done")
+    for i in range(steps):
+        runner.decode(1)
+        runner.tokens()
+        log(f"decode probe: step {i + 1}")
+    toks = runner.tokens()
+    runner.close()
+    return {"prompt": prompt_len, "steps": steps, "generated": [int(t) for t in toks[prompt_len:]]}
+
+
 def traffic_from_profile(kernel: str):
     """HBM bytes per launch of the headline kernel, from the committed rocprofv3
     PMC summary (FETCH_SIZE and WRITE_SIZE passes, each calibrated against a
@@ -715,8 +738,8 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "prefill_affine", "swiglu", "decode", "floor", "vendor",
-                                       "ops"],
+    ap.add_argument("--only", choices=["gemv", "prefill", "prefill_affine", "swiglu", "decode", "decode_probe",
+                                       "floor", "vendor", "ops"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
@@ -753,6 +776,8 @@ def main() -> int:
             out["prefill"] = [prefill(ctx, engine, 4096, 4096, steps=args.prefill_steps, use_graph=not args.no_graph)]
             out["prefill_affine"] = [prefill(ctx, engine, 4096, 4096, steps=args.prefill_steps, affine=True, x_f32=f,
                                              use_graph=not args.no_graph) for f in (False, True)]
+        elif args.only == "decode_probe":
+            out["decode_probe"] = decode_probe(ctx)
         elif args.only == "swiglu":
             out["swiglu"] = [swiglu(ctx, engine, m, use_graph=not args.no_graph) for m in (1, 8)]
         elif args.only == "vendor":
