@@ -606,7 +606,52 @@ def cpu_baseline(seconds: float):
             "sample": (f"{steps} per-token steps of the reference path (k-ascending f32 fma GEMV on the "
                        f"load-time-dequantized f32 weight, configs[1] shape 4096x4096 M=1) in {el:.1f} s; "
                        f"bytes counted as the int8 algorithmic bytes of the GPU step"),
-            "legs": [cpu_leg_config0(seconds / 2), cpu_leg_config3(seconds / 2)]}
+            "legs": [cpu_leg_config0(seconds / 2), cpu_leg_config3(seconds / 2), cpu_leg_config4(seconds / 2)]}
+
+
+def cpu_leg_config4(seconds: float) -> dict:
+    """configs[4] on host cores: the reference's per-token Linear path
+    (load-time f32 dequantization, then matmul_tiled's k-ascending f32 sums at
+    M = 1) through one LlamaBlock's seven Linears (q, k, v, o, gate, up, down
+    at the 1.1B shape) and the lm_head, each token timed; tokens/s =
+    1 / (22 x block + lm_head).  Attention, norms, RoPE and the pick are left
+    out (under 1 % of the work at 640 positions)."""
+    from oracle import oracle as orc
+    from rusty_amd import synth
+    from rusty_amd.llama import LLAMA_1B
+
+    cfg = LLAMA_1B
+    g = synth.rng(0)
+    refs = [orc.RefLinear(*synth.rowwise_weight(g, n, k), None, 0) for n, k in cfg.linear_shapes().values()]
+    head = orc.RefLinear(*synth.rowwise_weight(g, cfg.vocab, cfg.hidden), None, 0)
+    xs = {k: synth.activations(g, 1, k, dtype=np.float32) for k in {k for _, k in cfg.linear_shapes().values()}}
+
+    def block():
+        threads = 1
+        for r in refs:
+            threads = r.forward(xs[r.k])[1]
+        return threads
+
+    block()
+    head.forward(xs[cfg.hidden])
+    n, tb, t0 = 0, 0.0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds * 0.8:
+        a = time.perf_counter()
+        threads = block()
+        tb += time.perf_counter() - a
+        n += 1
+    nh, th, t1 = 0, 0.0, time.perf_counter()
+    while time.perf_counter() - t1 < seconds * 0.2 or nh == 0:
+        a = time.perf_counter()
+        head.forward(xs[cfg.hidden])
+        th += time.perf_counter() - a
+        nh += 1
+    per_tok = cfg.n_layers * tb / n + th / nh
+    return {"config": "configs[4]", "value": round(1.0 / per_tok, 3), "unit": "tok/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"one 1.1B block's 7 Linears timed over {n} tokens ({tb / n * 1e3:.1f} ms each) and the "
+                      f"lm_head over {nh} ({th / nh * 1e3:.1f} ms each), M = 1, f32 on the load-time-dequantized "
+                      f"weights; per token = 22 blocks + lm_head = {per_tok * 1e3:.0f} ms"}
 
 
 def _timed_forward(ref, x, y, seconds):

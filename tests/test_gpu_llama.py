@@ -161,6 +161,32 @@ def test_restart_and_single_token_prompt(ctx):
     r.close()
 
 
+def test_step_graph_captured_at_first_graph_step(ctx):
+    """The step graph is captured by the first step that runs in graph mode: a
+    runner that first steps as direct launches (no graph captured yet) and
+    then switches to graph steps gives the same tokens and logits, bit for
+    bit, as one that used the graph from the start (the same kernels in the
+    same order), and both match the oracle."""
+    w = synth_weights(TINY, seed=27)
+    prompt = np.random.default_rng(28).integers(0, TINY.vocab, 20)
+    a = LlamaRunner(ctx, TINY, w)
+    a.set_graph(False)
+    ta, la = run_collect(a, prompt, 6)
+    a.set_graph(True)
+    extra = []
+    for _ in range(4):
+        a.decode(1)
+        extra.append(a.logits())
+    ta = a.tokens()
+    a.close()
+    b = LlamaRunner(ctx, TINY, w)
+    tb, lb = run_collect(b, prompt, 10)
+    b.close()
+    np.testing.assert_array_equal(ta, tb)
+    np.testing.assert_array_equal(np.concatenate([la, np.stack(extra)]).view(np.uint32), lb.view(np.uint32))
+    check_steps(TINY, w, tb, lb, 20, 1e-2, "lazy graph")
+
+
 def test_invalid_arguments(ctx):
     w = synth_weights(TINY, seed=23)
     r = LlamaRunner(ctx, TINY, w)
