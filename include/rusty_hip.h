@@ -209,8 +209,10 @@ int rq_matmul_at(rq_ctx *ctx, const float *a, const float *b, float *out, int64_
  * 256-k batch whenever a value passes fp16's range (65504) -- so any finite
  * f32 row is served (at 3..16 rows a row whose values all lie below 6.1e-5
  * keeps fp16-subnormal precision); the GEMM rounds them to fp16 (the
- * fp16-MFMA prefill path; values past 65504 become infinite there), as it
- * does affine weights.  On the
+ * fp16-MFMA prefill path), each row scaled first by the power of two that
+ * puts its largest magnitude in [2^14, 2^15) and its outputs scaled back, so
+ * there too any finite row is served, at fp16 accuracy; it rounds affine
+ * weights to fp16 likewise.  On the
  * context's own stream (stream NULL) a GEMM with few tokens splits K over
  * more blocks using the context's workspace, so two such calls of one
  * context must not run concurrently (they cannot on one stream); on any

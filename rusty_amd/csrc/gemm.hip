@@ -157,7 +157,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                                                      int y_f16, int M, int N, int K, int tiles_m, int tiles_n,
                                                      int gm, int splits, float *__restrict__ skw,
                                                      int *__restrict__ skc, int group, const uint8_t *__restrict__ Wb,
-                                                     const float *__restrict__ scalesb, int n_split, RopeOut ro) {
+                                                     const float *__restrict__ scalesb, int n_split, RopeOut ro,
+                                                     const float *__restrict__ xscale) {
     static_assert(!ROPE || (BN == 64 && FMT == 0 && !PAIR), "rotary epilogue: one 64-wide head per tile");
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
@@ -306,6 +307,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     esc[io][g][r] = scl[wr < NL ? wr : 0];
                 }
             }
+    }
+    // f32 activations cast with a per-row power of two (xscale: 2^e per token
+    // row, the X rows holding x * 2^-e): the factor of every token row this
+    // lane's outputs cover, multiplied in by the epilogue (exact; 1 without
+    // xscale).  Requested here for the same reason as the scales.
+    float tfac[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int tr = m0 + wm * TM + j * 32 + fr;
+        tfac[j] = xscale ? xscale[tr < M ? tr : M - 1] : 1.0f;
     }
     // ROPE: the (cos, sin) of the pairs 4 (t % 8) .. + 3 at the positions of
     // the tile rows this thread writes (32 ps + t / 8), requested here for the
@@ -665,8 +676,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
-                    const float v0 = acc[i][j][4 * g] * sc[0], v1 = acc[i][j][4 * g + 1] * sc[1];
-                    const float v2 = acc[i][j][4 * g + 2] * sc[2], v3 = acc[i][j][4 * g + 3] * sc[3];
+                    const float tf = tfac[j];
+                    const float v0 = acc[i][j][4 * g] * sc[0] * tf, v1 = acc[i][j][4 * g + 1] * sc[1] * tf;
+                    const float v2 = acc[i][j][4 * g + 2] * sc[2] * tf, v3 = acc[i][j][4 * g + 3] * sc[3] * tf;
                     if constexpr (EB == 2) {
                         const h2_t lo = {(_Float16)v0, (_Float16)v1}, hi = {(_Float16)v2, (_Float16)v3};
                         *reinterpret_cast<uint2 *>(dst) =
@@ -767,7 +779,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     if (mm >= M) continue;
                     float v[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r];
+                    for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r] * tfac[j];
                     const size_t o = (size_t)mm * N + nb;
                     if (nb + 4 <= N && (N % 4) == 0) {
                         if (y_f16) {
@@ -813,7 +825,7 @@ struct GemmPair {
 template <int BM, int BN, bool PINGPONG, int S, int NW, int WGN, int KG = 1, bool W2 = false, bool PAIR = false>
 int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
                  int gm, int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{},
-                 const RopeOut *rope = nullptr) {
+                 const RopeOut *rope = nullptr, const float *xscale = nullptr) {
     const int64_t N = w.n_out, K = w.k_in;
     const int tiles_m = (int)cdiv(m, BM), tiles_n = (int)cdiv(N, BN);
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
@@ -829,7 +841,8 @@ int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *
         hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * splits)), dim3(64 * NW), 0, s, (const uint8_t *)w.codes,
                            scales, (const _Float16 *)x, y, yt == RQ_F16 ? 1 : 0, (int)m, (int)N, (int)K, tiles_m,
                            tiles_n, gm < 1 ? 1 : gm, (int)splits, ws.partials, ws.counters, fmt == 1 ? w.group : 64,
-                           pair.w, pair.scales, (int)(pair.n_split ? pair.n_split : N), rope ? *rope : RopeOut{});
+                           pair.w, pair.scales, (int)(pair.n_split ? pair.n_split : N), rope ? *rope : RopeOut{},
+                           xscale);
     };
     if constexpr (BN == 64 && !PAIR) {
         if (rope) {
@@ -894,14 +907,55 @@ int launch_affine_prep(const rq_qweight &w, float *table, hipStream_t s) {
 
 namespace {
 
-// f32 activations to fp16 (round to nearest even), 8 per thread per step.
-__global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, _Float16 *__restrict__ y, size_t n8) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
-        const float4 a = reinterpret_cast<const float4 *>(x)[2 * i], b = reinterpret_cast<const float4 *>(x)[2 * i + 1];
-        const half8 h = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-                         (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-        reinterpret_cast<half8 *>(y)[i] = h;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// f32 activation rows to fp16 (round to nearest even), one block per row: the
+// row is scaled by the power of two 2^-e that puts its largest magnitude in
+// [2^14, 2^15) and rs[row] = 2^e, which the GEMM's epilogue multiplies back
+// (exact).  Any finite row fits fp16 that way, small rows keep fp16's full
+// precision, and a row whose values all lie in fp16's normal range gives the
+// same products as a plain conversion (scaling by a power of two commutes
+// with rounding there).  The row is read twice (its maximum, then the
+// conversion; the second read hits L2), K % 8 == 0.
+__global__ __launch_bounds__(256) void k_cast_f16_rows(const float *__restrict__ x, _Float16 *__restrict__ y,
+                                                       float *__restrict__ rs, int K) {
+    __shared__ float wmax[4];
+    const size_t row = blockIdx.x;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + row * K);
+    half8 *yr = reinterpret_cast<half8 *>(y + row * K);
+    const int n8 = K / 8, t = threadIdx.x, lane = t & 63;
+    float amax = 0.0f;
+    for (int i = t; i < n8; i += 256) {
+        const float4 a = xr[2 * i], b = xr[2 * i + 1];
+        amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
     }
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
+    amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: each 16-lane row holds its maximum
+    const auto rl = [](float v, int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    };
+    amax = fmaxf(fmaxf(rl(amax, 0), rl(amax, 16)), fmaxf(rl(amax, 32), rl(amax, 48)));
+    if (lane == 0) wmax[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    // amax = f * 2^E, f in [0.5, 1); a zero, infinite or NaN maximum gives
+    // E = 0 (an inf or NaN stays one)
+    const int e = max(__builtin_amdgcn_frexp_expf(amax) - 15, -126);
+    for (int i = t; i < n8; i += 256) {
+        const float4 a = xr[2 * i], b = xr[2 * i + 1];
+        const half8 h = {(_Float16)__builtin_amdgcn_ldexpf(a.x, -e), (_Float16)__builtin_amdgcn_ldexpf(a.y, -e),
+                         (_Float16)__builtin_amdgcn_ldexpf(a.z, -e), (_Float16)__builtin_amdgcn_ldexpf(a.w, -e),
+                         (_Float16)__builtin_amdgcn_ldexpf(b.x, -e), (_Float16)__builtin_amdgcn_ldexpf(b.y, -e),
+                         (_Float16)__builtin_amdgcn_ldexpf(b.z, -e), (_Float16)__builtin_amdgcn_ldexpf(b.w, -e)};
+        yr[i] = h;
+    }
+    if (t == 0) rs[row] = __builtin_amdgcn_ldexpf(1.0f, e);
 }
 
 // Whether a grid of bm x bn tiles over m x N still has >= 2/3 as many tiles as
@@ -913,7 +967,8 @@ bool tile_fills(int64_t m, int64_t N, int64_t cus, int bm, int bn) {
 
 // The fp16-activation GEMM over m rows, tile chosen by shape.
 int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x, void *y, rq_dtype yt, int64_t m,
-               int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{}) {
+               int64_t cus, const GemmWorkspace &ws, hipStream_t s, const GemmPair &pair = GemmPair{},
+               const float *xscale = nullptr) {
     const int64_t N = w.n_out;
     // The largest tile whose grid still has >= 2/3 as many tiles as the device
     // has CUs: a block streams its X and W panels through one CU at a latency-
@@ -940,10 +995,16 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
             return launch_tiled<128, 128, true, 4, 8, 2, 2, true, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, pair);
         return RQ_ERR_UNSUPPORTED;
     }
-    if (fills(128, 256)) return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
-    if (fills(128, 128)) return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
-    if (fills(128, 64)) return launch_tiled<128, 64, true, 6, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
-    return launch_tiled<64, 64, true, 4, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s);
+    const GemmPair np{};
+    if (fills(128, 256))
+        return launch_tiled<128, 256, true, 4, 8, 4, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr,
+                                                              xscale);
+    if (fills(128, 128))
+        return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr,
+                                                              xscale);
+    if (fills(128, 64))
+        return launch_tiled<128, 64, true, 6, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
+    return launch_tiled<64, 64, true, 4, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
 }
 
 }  // namespace
@@ -1031,19 +1092,21 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
         used = sc_bytes;
     }
     if (xt == RQ_F16) return gemm_tiles(w, scales, fmt, x, y, yt, m, cus, ws, s);
-    // f32 activations: cast a chunk of rows (a multiple of 128) to fp16, multiply it
-    const int64_t chunk = std::min<int64_t>(m, (int64_t)((ws.prep_bytes - used) / ((size_t)K * 2)) / 128 * 128);
+    // f32 activations: cast a chunk of rows (a multiple of 128) to fp16, each
+    // row scaled by a power of two (the factors after the rows), multiply it
+    const size_t row_bytes = (size_t)K * 2 + 4;
+    const int64_t chunk = std::min<int64_t>(m, (int64_t)((ws.prep_bytes - used - 256) / row_bytes) / 128 * 128);
     if (chunk < std::min<int64_t>(m, 128)) return RQ_ERR_UNSUPPORTED;
     _Float16 *x16 = reinterpret_cast<_Float16 *>(prep + used);
+    float *xs = reinterpret_cast<float *>(prep + used + (((size_t)chunk * K * 2 + 255) & ~size_t(255)));
     const size_t eb = yt == RQ_F16 ? 2 : 4;
     for (int64_t r0 = 0; r0 < m; r0 += chunk) {
         const int64_t mc = std::min(chunk, m - r0);
-        const size_t n8 = (size_t)mc * (size_t)K / 8;  // K % 64 == 0
-        const unsigned blocks = (unsigned)std::min<size_t>(std::max<size_t>(cdiv((int64_t)n8, 256), 1), 8192);
-        hipLaunchKernelGGL(k_cast_f16, dim3(blocks), dim3(256), 0, s, static_cast<const float *>(x) + r0 * K, x16, n8);
+        hipLaunchKernelGGL(k_cast_f16_rows, dim3((unsigned)mc), dim3(256), 0, s, static_cast<const float *>(x) + r0 * K,
+                           x16, xs, (int)K);
         RQ_LAUNCH_CHECK();
         const int st = gemm_tiles(w, scales, fmt, x16, static_cast<uint8_t *>(y) + (size_t)r0 * (size_t)N * eb, yt, mc,
-                                  cus, ws, s);
+                                  cus, ws, s, GemmPair{}, xs);
         if (st != RQ_OK) return st;
     }
     return RQ_OK;

@@ -5,9 +5,11 @@ Tolerances (stated here, reported by every test):
   * f32 output: max|dy| / max|y| <= 1e-5
   * fp16 output: |dy| <= 2e-3*|y| + 2e-3*max|y| elementwise
 The truth is computed from the same fp16-rounded X and the exactly dequantized
-weight.  Full prefill sizes are checked on sampled rows that cover every
-128-row tile and every row position inside a tile, plus a column-checksum
-(sum over all tokens, a linear invariant) that covers every output row.
+weight.  The configs[3] shapes are checked on every output element (per-row
+codes at all three, affine codes at 4096x4096); the other full prefill sizes
+on sampled rows that cover every 128-row tile and every row position inside a
+tile, plus a column-checksum (sum over all tokens, a linear invariant) that
+covers every output row.
 """
 import numpy as np
 import pytest
@@ -255,6 +257,31 @@ def _check_prefill(y, x, q, s, name):
     assert np.all(np.abs(col_dev - col_truth) <= bound), float((np.abs(col_dev - col_truth) / bound).max())
 
 
+# configs[3] at full size, every output element against the f64 truth (the
+# exactly dequantized weight, W = q * s or u * s + b in f64, multiplied by the
+# fp16-rounded activations with f64 BLAS), per-row codes at the three shapes
+# and the reference's affine codes at 4096x4096.
+@pytest.mark.parametrize("n,k,fmt", [(4096, 4096, 0), (11008, 4096, 0), (4096, 11008, 0), (4096, 4096, 1)])
+def test_config4_prefill_every_element(ctx, engine, n, k, fmt):
+    g = synth.rng(7000 + n + k + fmt)
+    x = synth.activations(g, 2048, k, sigma=0.5)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n, k)
+        W = QuantizedTensor.rowwise(ctx, q, s)
+        wd = q.astype(np.float64) * s.astype(np.float64)[:, None]
+    else:
+        q, s, b = synth.affine_weight(g, n, k)
+        W = QuantizedTensor.affine(ctx, q, s, b)
+        rep = lambda a: np.repeat(a.astype(np.float64).reshape(n, k // 64), 64, axis=1)  # noqa: E731
+        wd = q.astype(np.float64) * rep(s) + rep(b)
+    y = qmm(ctx, engine, W, x, np.float16)
+    truth = x.astype(np.float64) @ wd.T
+    del wd
+    max_abs, rel, ok = f16_tol_check(y, truth)
+    report(f"C4 every element 2048x{n}x{k} fmt={fmt}", max_abs, rel)
+    assert ok
+
+
 @pytest.mark.parametrize("n,k", [(4096, 4096), (11008, 4096), (4096, 11008)])
 def test_config4_prefill(ctx, engine, n, k):
     g = synth.rng(n + k)
@@ -410,8 +437,39 @@ def test_config4_prefill_f32_activations(ctx, engine):
     _check_rows(y, x, (q, s, None, 0), "C4 rowwise 2048x4096x4096 x=float32")
 
 
+# f32 activations past fp16's range on the GEMM path (m > 16): each row is cast
+# with its own power-of-two scale (largest magnitude in [2^14, 2^15)) that the
+# epilogue multiplies back, so rows with entries of 1e5..3e5 (fp16 ends at
+# 65504) and a row of values ~1e-6 (below fp16's normal range) are held to the
+# fp16 bar of their own rows against the f64 truth of the f32 input;
+# 300 tokens: 128x64 tiles, 40 tokens: split-K 64x64 tiles.
+@pytest.mark.parametrize("m,n,k,fmt", [(300, 1024, 4096, 0), (40, 4096, 4096, 0), (300, 1024, 4096, 1)])
+def test_gemm_f32_activations_past_fp16_range(ctx, engine, m, n, k, fmt):
+    g = synth.rng(9100 + m + fmt)
+    x = synth.activations(g, m, k, sigma=0.5, dtype=np.float32)
+    for r in range(0, m, 3):
+        j = g.choice(k, size=3, replace=False)
+        x[r, j] = (g.choice([-1.0, 1.0], 3) * g.uniform(1e5, 3e5, 3)).astype(np.float32)
+    x[1] = (x[1] * 1e-6).astype(np.float32)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n, k)
+        b, W = None, QuantizedTensor.rowwise(ctx, q, s)
+    else:
+        q, s, b = synth.affine_weight(g, n, k)
+        W = QuantizedTensor.affine(ctx, q, s, b)
+    truth = orc.qlinear_truth(q, s, b, x, fmt)
+    y = qmm(ctx, engine, W, x, np.float32)
+    assert np.isfinite(y).all()
+    worst = 0.0
+    for r in range(m):
+        max_abs, rel, ok = f16_tol_check(y[r], truth[r])
+        worst = max(worst, max_abs / np.abs(truth[r]).max())
+        assert ok, (r, max_abs, rel)
+    report(f"f32 x past fp16 range {m}x{n}x{k} fmt={fmt}: worst row max|dy|/max|y|", worst, worst)
+
+
 # every tile, split-K, group 128, and f32 activations in two chunks of the preparation area
-# (3000 x 16384 f32 -> fp16 is 98 MB: chunks of 2048 and 952 rows)
+# (3000 x 16384 f32 -> fp16 is 98 MB: two chunks)
 @pytest.mark.parametrize("m,n,k,fmt,group,xdt", [
     (17, 300, 1024, 1, 64, np.float16),     # 64x64, split-K
     (9, 4096, 4096, 1, 64, np.float32),     # 9 tokens, f32: the GEMM (split-K)
