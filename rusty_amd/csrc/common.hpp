@@ -148,8 +148,8 @@ int launch_gemv_decode_qkv_rope(const rq_qweight &w, const float *x, const _Floa
                                 const RopeDecode &rd, hipStream_t s);
 // y[n] += sum_k W[n, k] x[k] (m = 1, f32 y) with x the decode attention output
 // combined in the prologue from n_split (1, 2, 4 or 8) partial softmaxes per head
-// of head_dim elements: partials = acc[head][n_split][head_dim] f32, then
-// (m, l)[head][n_split] float2.
+// of head_dim elements: partials = o[head][n_split][head_dim] fp16 (each
+// split's output, normalised by its own sum l), then (m, l)[head][n_split] float2.
 int launch_gemv_decode_attn_add(const rq_qweight &w, const float *partials, int n_split, int head_dim, float *y,
                                 hipStream_t s);
 int launch_swiglu_mfma(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int m,

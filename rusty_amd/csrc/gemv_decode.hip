@@ -87,9 +87,10 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // in flight, so the norm costs no launch and hides under the weight stream.
 // SA > 0 (m = 1): the activation row is decode attention's output, combined
 // in the prologue from SA partial softmaxes per head (the attention kernel's
-// split over positions): Xf holds acc[head][SA][attn_hd] (f32) followed by
-// (m, l)[head][SA] (float2); x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
-// M = max_s m_s, rounded to fp16 and shared through LDS like the norm's row.
+// split over positions): Xf holds o[head][SA][attn_hd] (fp16, each split's
+// output normalised by its own sum) followed by (m, l)[head][SA] (float2);
+// x = sum_s w_s o_s / sum_s w_s, w_s = e^(m_s - M) l_s, M = max_s m_s, rounded
+// to fp16 and shared through LDS like the norm's row.
 // ROPE (with NORM, m = 1): the weight is a Llama layer's packed [q; k; v]
 // (rd.hd rows per head) and the block's local rows come in rotate-half pairs:
 // local rows 2p and 2p + 1 are rows d and d + hd/2 of one head, global pair
@@ -162,14 +163,14 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
     float pe[XF ? CPT : 1][XF ? M : 1];
     uint4 xf4[NORM ? NL : 1][4], nw4[NORM ? NL : 1][2];
     // SA: 8-element pieces of the row, piece u by thread u % DT: SA (m, l)
-    // pairs of its head and SA x 8 accumulator values
+    // pairs of its head and SA x 8 fp16 partial outputs
     constexpr int NU = (2 * XC + DT - 1) / DT;
     constexpr int SAL = SA > 0 ? SA : 1;
-    uint4 pacc[SA > 0 ? NU : 1][SAL][2], pml[SA > 0 ? NU : 1][(SAL + 1) / 2];
+    uint4 pacc[SA > 0 ? NU : 1][SAL][1], pml[SA > 0 ? NU : 1][(SAL + 1) / 2];
     if constexpr (SA > 0) {
         const int nh = K / attn_hd;
-        const auto racc = make_rsrc(Xf, (uint32_t)nh * SA * (uint32_t)attn_hd * 4u);
-        const auto rml = make_rsrc(Xf + (size_t)nh * SA * attn_hd, (uint32_t)nh * SA * 8u);
+        const auto racc = make_rsrc(Xf, (uint32_t)nh * SA * (uint32_t)attn_hd * 2u);
+        const auto rml = make_rsrc(Xf + (size_t)nh * SA * attn_hd / 2, (uint32_t)nh * SA * 8u);
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
             const int u = t + DT * j;
@@ -180,9 +181,8 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
                 pml[j][q] = bload<0>(rml, live ? (uint32_t)(h * SA + 2 * q) * 8u : kOOB);
 #pragma unroll
             for (int sp = 0; sp < SAL; ++sp) {
-                const uint32_t off = live ? ((uint32_t)(h * SA + sp) * attn_hd + d0) * 4u : kOOB;
+                const uint32_t off = live ? ((uint32_t)(h * SA + sp) * attn_hd + d0) * 2u : kOOB;
                 pacc[j][sp][0] = bload<0>(racc, off);
-                pacc[j][sp][1] = bload<0>(racc, off + 16);
             }
         }
     } else if constexpr (NORM) {
@@ -364,8 +364,8 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             float wgt[SAL], den = 0.0f;
 #pragma unroll
             for (int sp = 0; sp < SAL; ++sp) {
-                wgt[sp] = expf(mv[sp] - mx);  // an empty split's m = -inf weighs 0
-                den = __builtin_fmaf(wgt[sp], lv[sp], den);
+                wgt[sp] = expf(mv[sp] - mx) * lv[sp];  // an empty split's m = -inf weighs 0
+                den += wgt[sp];
             }
             const float inv = 1.0f / den;
             float o[8];
@@ -373,10 +373,14 @@ __global__ __launch_bounds__(DT) void k_gemv_decode(const uint8_t *__restrict__ 
             for (int e = 0; e < 8; ++e) o[e] = 0.0f;
 #pragma unroll
             for (int sp = 0; sp < SAL; ++sp) {
-                const uint4 a = pacc[j][sp][0], b = pacc[j][sp][1];
-                const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const uint4 a = pacc[j][sp][0];
+                const uint32_t wd[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wgt[sp], __builtin_bit_cast(float, wd[e]), o[e]);
+                for (int e = 0; e < 4; ++e) {
+                    const h2_t hv = __builtin_bit_cast(h2_t, wd[e]);
+                    o[2 * e] = __builtin_fmaf(wgt[sp], (float)hv.x, o[2 * e]);
+                    o[2 * e + 1] = __builtin_fmaf(wgt[sp], (float)hv.y, o[2 * e + 1]);
+                }
             }
             uint32_t hv[4];
 #pragma unroll

@@ -48,7 +48,8 @@ struct rq_llama {
     rq_qweight lm_head{};
     void *owned = nullptr;  // packed qkv weights + step state, one allocation
     float *x = nullptr, *qkv_out = nullptr, *logits = nullptr;
-    float *part = nullptr;  // attention partials: acc [n_heads][n_split][head_dim], then (m, l) pairs
+    // attention partials: fp16 acc / l [n_heads][n_split][head_dim], then f32 (m, l) pairs
+    float *part = nullptr;
     int n_split = 1;        // attention blocks per query head
     _Float16 *h = nullptr, *kc = nullptr, *vc = nullptr;
     int *tokens = nullptr, *pos = nullptr, *n_prompt = nullptr;
@@ -134,11 +135,15 @@ __device__ __forceinline__ void widen8(const uint4 u, float *f) {
 // of one pass (PASS positions): block (head hd, split sp) of a grid of
 // n_heads * S takes tiles sp, sp + S, sp + 2 S, ... of positions 0..pos and
 // writes its partial softmax -- the running max m, the sum l of
-// exp(score - m) and the unnormalised accumulator acc[d] = sum exp(score - m)
-// * v[d] -- to part[(hd * S + sp) * HD + d] and ml[hd * S + sp] = (m, l).  A
-// block with no position (sp * PASS > pos) writes (-inf, 0, 0).  The
+// exp(score - m), and its output o[d] = acc[d] / l for the unnormalised
+// accumulator acc[d] = sum exp(score - m) * v[d] -- as fp16 o to
+// part[(hd * S + sp) * HD + d] and f32 ml[hd * S + sp] = (m, l).  A block
+// with no position (sp * PASS > pos) writes o = 0, (m, l) = (-inf, 0).  The
 // consumer (the o-projection GEMV's prologue) combines the S partials of a
-// head: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s, M = max_s m_s.
+// head: out = sum_s w_s o_s / sum_s w_s, w_s = e^(m_s - M) l_s,
+// M = max_s m_s.  Normalised, o is within v's range, so fp16 holds it to
+// 2^-11 (the combined row is rounded to fp16 anyway); half the bytes of f32
+// partials, which every o-projection block reads (step +1.2 %).
 //
 // The q/k/v projection before it (launch_gemv_decode_qkv_rope) has already
 // rotated q and k (RoPE, kernels.wgsl:60-79) and appended this position's
@@ -256,7 +261,8 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
     // sum P.V partials over the lanes holding the same chunk: within a 16-lane
     // row (HD = 64: two rows of 8 chunks, row_ror 8 pairs lane i with i + 8),
     // then over the four rows of each wave and over waves in LDS, each wave's
-    // sums weighted by e^(m_w - M), M the block's max
+    // sums weighted by e^(m_w - M), M the block's max; stored divided by the
+    // block's sum l (0 for a block with no position)
     if constexpr (CH == 8) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] += dpp<0x128>(acc[e]);
@@ -287,7 +293,7 @@ __global__ __launch_bounds__(ATT) void k_attn_decode(const float *__restrict__ q
                 L = fmaf(f, reds[i], L);
             }
         }
-        part[slot * HD + t] = sum;
+        reinterpret_cast<_Float16 *>(part)[slot * HD + t] = (_Float16)(L > 0.0f ? sum / L : 0.0f);
         if (t == 0) ml[slot] = make_float2(M, L);
     }
 }
@@ -435,7 +441,8 @@ int enqueue_step(rq_llama *md, hipStream_t s) {
         rd.max_seq = c.max_seq;
         if ((st = launch_gemv_decode_qkv_rope(L.qkv, md->x, L.attn_norm, c.norm_eps, rd, s)) != RQ_OK) return st;
         const int S = md->n_split;
-        float2 *ml = reinterpret_cast<float2 *>(md->part + (size_t)c.n_heads * S * c.head_dim);
+        // (m, l) pairs after the fp16 partials (n_heads * S * head_dim halves)
+        float2 *ml = reinterpret_cast<float2 *>(md->part + (size_t)c.n_heads * S * c.head_dim / 2);
         if (c.head_dim == 64)
             hipLaunchKernelGGL(k_attn_decode<64>, dim3(c.n_heads * S), dim3(ATT), 0, s, md->qkv_out,
                                md->kc + l * kv_layer, md->vc + l * kv_layer, md->pos, md->part, ml, c.n_heads,
