@@ -7,8 +7,11 @@
 // so the products go to v_mfma_f32_16x16x32_f16 (16 features x 16 tokens x 32
 // k per instruction; MFMA throughput is far from the limit here):
 //  * One block of NWV waves per 16 weight rows (SwiGLU: 8 gate + the same 8
-//    up rows).  Wave w takes the 256-k batches w, w + NWV, ..., counted from
-//    a per-block rotation that staggers the blocks' activation reads.
+//    up rows), or per two such row tiles where the launcher's measurements
+//    favour it (tall weights, SwiGLU pairs): the activation block, re-read by
+//    every block, is then read once for 32 rows.  Wave w takes the 256-k
+//    batches w, w + NWV, ..., counted from a per-block rotation that
+//    staggers the blocks' activation reads.
 //  * Weights are loaded as 4 rows x 256 contiguous bytes per instruction
 //    (lane chunk lane % 16 of row 4 i + lane / 16): against loading the MFMA
 //    operand layout directly (16 rows x 64 B per instruction) the weight
@@ -22,9 +25,10 @@
 //    barrier keeps the compiler from interleaving them with the conversions),
 //    and the next batch's loads are in flight while the current batch is
 //    multiplied.  Tokens >= m, rows >= N and k >= K read as zero.
-//  * NWV = 8 where the grid is at most two blocks per CU and K <= 4096 (one
-//    block per CU needs the eight waves' loads in flight), else NWV = 4: more
-//    resident blocks per CU did better at K = 11008 or N = 11008.
+//  * NWV = 8 where the one-tile grid is at most two blocks per CU and
+//    K <= 4096 (one block per CU needs the eight waves' loads in flight), else
+//    NWV = 4: more resident blocks per CU did better at K = 11008 or
+//    N = 11008.
 //  * The weight is expanded exactly in registers: XOR 0x80, v_perm_b32 under
 //    exponent 0x64 (fp16 1152+q), v_pk_add_f16 -1152.
 //  * The waves' 16x16 partial sums meet in LDS once; scale, fp16/f32 store
@@ -91,9 +95,9 @@ __device__ __forceinline__ half8 u8x8_affine(uint32_t lo, uint32_t hi, float s, 
 // One batch of a wave's operands: 256 k of the block's 16 weight rows, as
 // loaded (4 rows x 256 B per instruction), and the activations of the 8 MFMAs
 // that consume them (16 B per lane per MFMA, already in operand layout).
-template <int FMT, bool XF>
+template <int FMT, bool XF, int RT = 1>
 struct Batch {
-    uint4 w[4], x[XF ? 16 : 8];  // XF: 8 f32 activations (two loads) per MFMA
+    uint4 w[RT][4], x[XF ? 16 : 8];  // XF: 8 f32 activations (two loads) per MFMA
     // affine: the four group scales / biases of MFMA row fr (fp16 expansion);
     // affine with XF: those of output rows 4 q + r, r < 4 (applied after the MFMAs)
     float4 s[FMT == 1 && XF ? 4 : 1], b[FMT == 1 && XF ? 4 : 1];
@@ -159,47 +163,63 @@ __device__ __forceinline__ float wave_max(float v) {
 // batch's largest magnitude in [2^14, 2^15), its sums scaled back by 2^S.
 // XFIRST: each batch's activation loads are issued before its weight loads
 // (see launch_mfma).
-template <bool SWI, int NWV, int FMT = 0, bool XF = false, bool XFIRST = false>
+// RT: row tiles per block (per-row codes, fp16 activations): tile t covers
+// the block's rows t * RB .. (SwiGLU: 8 gate and the same 8 up rows each);
+// every activation fragment a wave loads feeds the MFMAs of all RT tiles, so
+// a block reads the activation block once for RT times the weight rows.
+template <bool SWI, int NWV, int FMT = 0, bool XF = false, bool XFIRST = false, int RT = 1>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict__ W, const float *__restrict__ scales,
                                                   const int8_t *__restrict__ W2, const float *__restrict__ scales2,
                                                   const void *__restrict__ X, void *__restrict__ Yv, int y_f16,
                                                   int m_act, int N, int K, const float *__restrict__ biases,
                                                   const float *__restrict__ biases2) {
-    constexpr int RB = SWI ? 8 : 16;  // output rows per block
-    __shared__ floatx4 red[NWV][64];
-    // per wave: the 16 rows x 256 k of the batch being multiplied, rows of
-    // 256 B with 16-byte chunk c of row r stored at chunk c ^ r
-    __shared__ __attribute__((aligned(16))) uint8_t wt[NWV][16 * 256];
+    static_assert(RT == 1 || (FMT == 0 && !XF), "row tiles: per-row codes, fp16 activations");
+    static_assert(RT <= NWV, "one wave finishes each row tile");
+    constexpr int RB = SWI ? 8 : 16;  // output rows per row tile
+    __shared__ floatx4 red[NWV][RT][64];
+    // per wave and tile: the 16 rows x 256 k of the batch being multiplied,
+    // rows of 256 B with 16-byte chunk c of row r stored at chunk c ^ r
+    __shared__ __attribute__((aligned(16))) uint8_t wt[NWV][RT][16 * 256];
 
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);  // scalar: the batch loop branches uniformly
     const int fr = lane % 16, q = lane / 16;  // MFMA operand row (weight row / token) and lane group
-    const int n0 = blockIdx.x * RB;
-    const int rows_here = min(RB, N - n0);
+    const int n0 = blockIdx.x * RB * RT;
+    int rht[RT];  // rows of each tile (0 past the weight)
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) rht[tt] = max(0, min(RB, N - (n0 + tt * RB)));
+    const int rows_here = rht[0];
     // The row scales of this lane's outputs (rows 4 q + r), requested with the
     // first weight batch (below): loaded in the epilogue, each output waited
     // for its scale after the reduction (a round trip per output row on the
     // block's tail).
-    float sc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sc2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sc[RT][4], sc2[RT][4];
     auto load_scales = [&]() {
         if constexpr (FMT == 0) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int f = 4 * q + r, row = n0 + (f < rows_here ? f : 0);
-                sc[r] = scales[row];
-                if constexpr (SWI) sc2[r] = scales2[row];
-            }
+            for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 4 * q + r, row = (f < rht[tt] ? n0 + tt * RB + f : 0);
+                    sc[tt][r] = scales[row];
+                    if constexpr (SWI) sc2[tt][r] = scales2[row];
+                }
         }
     };
-    const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
-    const auto rw2 = make_rsrc((SWI ? W2 : W) + (size_t)n0 * K, (uint32_t)rows_here * (uint32_t)K);
+    __amdgpu_buffer_rsrc_t rw[RT], rw2[RT];
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+        const size_t r0 = (size_t)(n0 + tt * RB) * K;
+        rw[tt] = make_rsrc(W + (rht[tt] ? r0 : 0), (uint32_t)rht[tt] * (uint32_t)K);
+        rw2[tt] = make_rsrc((SWI ? W2 : W) + (rht[tt] ? r0 : 0), (uint32_t)rht[tt] * (uint32_t)K);
+    }
     const auto rx = make_rsrc(X, (uint32_t)m_act * (uint32_t)K * (XF ? 4u : 2u));
     // Weight loads: instruction i covers rows 4 i + q, 256 contiguous bytes
     // each (lane chunk fr); SwiGLU: instructions 0-1 the gate rows 0-7, 2-3
     // the up rows 0-7.  A row past the weight, or k past K (which would fall
     // into the next row), reads as zero.
     const uint32_t xbase = ((uint32_t)fr * (uint32_t)K + 8u * (uint32_t)q) * (XF ? 4u : 2u);
-    uint8_t *wl = wt[wave];
+    uint8_t *wl = wt[wave][0];
     const int nb = (K + 255) / 256;  // 256-k batches; wave w takes batches w, w + NWV, ...
     // ... counted from this block's rotation brot (mod nb).  Every block reads
     // all of X: unrotated, the blocks that share an XCD's L2 (consecutive
@@ -212,7 +232,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     const int brot = (int)((blockIdx.x >> 3) * 5u + (blockIdx.x & 7u)) % nb;
 
     const int Gpr = K / 64;  // affine groups per row
-    auto load = [&](Batch<FMT, XF> &b, int bi) {
+    auto load = [&](Batch<FMT, XF, RT> &b, int bi) {
         int bb = bi + brot;
         bb -= bb >= nb ? nb : 0;
         const uint32_t k0 = (uint32_t)bb * 256u;
@@ -245,12 +265,14 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         }
         auto wloads = [&]() {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the weight block
-                const bool live = klive && r < rows_here;
-                const uint32_t off = (uint32_t)r * (uint32_t)K + k0 + 16u * (uint32_t)fr;
-                b.w[i] = bload<2>(SWI && i >= 2 ? rw2 : rw, live ? off : kOOB);
-            }
+            for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = SWI ? (4 * i + q) % 8 : 4 * i + q;  // row within the tile
+                    const bool live = klive && r < rht[tt];
+                    const uint32_t off = (uint32_t)r * (uint32_t)K + k0 + 16u * (uint32_t)fr;
+                    b.w[tt][i] = bload<2>(SWI && i >= 2 ? rw2[tt] : rw[tt], live ? off : kOOB);
+                }
         };
         auto xloads = [&]() {
 #pragma unroll
@@ -273,23 +295,31 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
             xloads();
         }
     };
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 acct[RT];
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) acct[tt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 &acc = acct[0];
     // Transpose through the wave's LDS slice: lane (fr, q) of MFMA j takes the
     // 8 codes of row fr at k = 32 j + 8 q, the k order of its activations.
     // Only this wave touches the slice, and LDS operations of a wave complete
     // in order, so no barrier is needed around it.
-    auto mma = [&](const Batch<FMT, XF> &b) {
+    auto mma = [&](const Batch<FMT, XF, RT> &b) {
+        uint2 at[RT][8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 4 * i + q;
-            *reinterpret_cast<uint4 *>(wl + r * 256 + ((fr ^ r) << 4)) = b.w[i];
-        }
-        uint2 a[8];
+        for (int tt = 0; tt < RT; ++tt) {
+            uint8_t *wlt = wl + tt * (16 * 256);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = 2 * j + (q >> 1);
-            a[j] = *reinterpret_cast<const uint2 *>(wl + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * i + q;
+                *reinterpret_cast<uint4 *>(wlt + r * 256 + ((fr ^ r) << 4)) = b.w[tt][i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = 2 * j + (q >> 1);
+                at[tt][j] = *reinterpret_cast<const uint2 *>(wlt + fr * 256 + ((c ^ fr) << 4) + 8 * (q & 1));
+            }
         }
+        const uint2 *a = at[0];
         if constexpr (XF) {
             // f32 activations: the batch as loaded, then (rarely) again scaled
             auto mma_x = [&](auto scaled, int sh) {
@@ -376,10 +406,14 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            half8 av;
-            if constexpr (FMT == 1) av = u8x8_affine(a[j].x, a[j].y, sg[j / 2], cg[j / 2]);
-            else av = i8x8_to_half8(a[j].x, a[j].y);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acc, 0, 0, 0);
+#pragma unroll
+            for (int tt = 0; tt < RT; ++tt) {
+                half8 av;
+                if constexpr (FMT == 1) av = u8x8_affine(a[j].x, a[j].y, sg[j / 2], cg[j / 2]);
+                else av = i8x8_to_half8(at[tt][j].x, at[tt][j].y);
+                acct[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8, b.x[j]), acct[tt], 0,
+                                                                   0, 0);
+            }
         }
     };
 
@@ -390,7 +424,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
     // the branch, and the prefetch is lost).  mb, the wave's batch count, is
     // wave-uniform.
     const int mb = (nb - wave + NWV - 1) / NWV;
-    Batch<FMT, XF> A, B;
+    Batch<FMT, XF, RT> A, B;
     if (mb > 0) {
         load(A, wave);
         load_scales();
@@ -413,14 +447,19 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         }
     }
 
-    // acc = D[feature 4 q + r][token fr], partial over this wave's groups.
-    red[wave][lane] = acc;
+    // acct[t] = D[feature 4 q + r][token fr] of tile t, partial over this
+    // wave's groups; wave t finishes tile t.
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) red[wave][tt][lane] = acct[tt];
     __syncthreads();
-    if (wave == 0) {
-        floatx4 v = red[0][lane];
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+        if (wave != tt) continue;
+        const int nt = n0 + tt * RB, rh = rht[tt];
+        floatx4 v = red[0][tt][lane];
 #pragma unroll
         for (int w = 1; w < NWV; ++w) {
-            const floatx4 o = red[w][lane];
+            const floatx4 o = red[w][tt][lane];
             v[0] += o[0];
             v[1] += o[1];
             v[2] += o[2];
@@ -429,16 +468,16 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         const int m = fr;
         if constexpr (SWI) {
             // gate rows 0..7 sit in lane groups 0-1, up rows 8..15 in groups 2-3
-            red[0][lane] = v;
+            red[0][tt][lane] = v;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            const floatx4 u = red[0][(lane + 32) % 64];
+            const floatx4 u = red[0][tt][(lane + 32) % 64];
             if (q < 2 && m < m_act) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int f = 4 * q + r;
-                    if (f < rows_here) {
-                        const float h = FMT == 1 ? silu(v[r]) * u[r] : silu(v[r] * sc[r]) * (u[r] * sc2[r]);
-                        reinterpret_cast<_Float16 *>(Yv)[(size_t)m * N + n0 + f] = (_Float16)h;
+                    if (f < rh) {
+                        const float h = FMT == 1 ? silu(v[r]) * u[r] : silu(v[r] * sc[tt][r]) * (u[r] * sc2[tt][r]);
+                        reinterpret_cast<_Float16 *>(Yv)[(size_t)m * N + nt + f] = (_Float16)h;
                     }
                 }
             }
@@ -446,9 +485,9 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int f = 4 * q + r;
-                if (f < rows_here) {
-                    const float y = FMT == 1 ? v[r] : v[r] * sc[r];
-                    const size_t o = (size_t)m * N + n0 + f;
+                if (f < rh) {
+                    const float y = FMT == 1 ? v[r] : v[r] * sc[tt][r];
+                    const size_t o = (size_t)m * N + nt + f;
                     if (y_f16) reinterpret_cast<_Float16 *>(Yv)[o] = (_Float16)y;
                     else reinterpret_cast<float *>(Yv)[o] = y;
                 }
@@ -470,29 +509,49 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
     if (affine && (w.group != 64 || K % 256 != 0 || (int64_t)N * (K / 64) * 4 > 0xffffffffll)) return RQ_ERR_UNSUPPORTED;
     if (w2 && (w2->format != w.format || !aligned(w2->codes, 16) || (affine && w2->group != w.group)))
         return RQ_ERR_UNSUPPORTED;
-    const int64_t blocks = cdiv(N, w2 ? 8 : 16);
-    auto go = [&](auto nwv, auto fmt, auto xfc) {
-        constexpr int NW = decltype(nwv)::value, F = decltype(fmt)::value;
+    // Two row tiles per block (per-row codes, fp16 activations): each block
+    // reads the activation block (m x K fp16, re-read by every block) once for
+    // twice the weight rows.  Taken where it measured faster (us, rotating
+    // copies past the Infinity Cache; one tile -> two):
+    //   gate/up pairs 11008 x 4096 (1376 tiles), 4 waves: SwiGLU m = 4 / 8 / 16
+    //     30.1 -> 29.7, 33.1 -> 31.5, 44.6 -> 37.5 (whole MLP)
+    //   8192 x 4096 (512 tiles), 8 waves: m = 8 10.27 -> 8.42
+    //   11008 x 4096 (688 tiles), 4 waves: m = 16 16.86 -> 15.56, but
+    //     m = 4 / 8 11.61 -> 13.18, 12.55 -> 13.9 (344 blocks leave the second
+    //     round of the grid a third full); 11264 x 2048 likewise
+    //   4096 x 4096 (256 tiles): 128 blocks, m = 8 6.04 -> 7.33
+    const int64_t rows_tile = w2 ? 8 : 16, blocks1 = cdiv(N, rows_tile);
+    const bool two = !affine && !xf &&
+                     (w2 ? blocks1 >= 512 : (blocks1 > 256 && blocks1 <= 512) || (m > 8 && blocks1 > 512));
+    const int64_t blocks = two ? cdiv(N, 2 * rows_tile) : blocks1;
+    auto go = [&](auto nwv, auto fmt, auto xfc, auto rtc) {
+        constexpr int NW = decltype(nwv)::value, F = decltype(fmt)::value, RT = decltype(rtc)::value;
         constexpr bool XF = decltype(xfc)::value;
         if (w2)
-            hipLaunchKernelGGL((k_gemv_mfma<true, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
+            hipLaunchKernelGGL((k_gemv_mfma<true, NW, F, XF, false, RT>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
                                (const int8_t *)w.codes, w.scales, (const int8_t *)w2->codes, w2->scales, x, y, 1, m,
                                (int)N, (int)K, w.biases, w2->biases);
         else {
             constexpr bool XFP = NW == 8 && F == 0 && !XF;  // the activation-first variant exists
             if (XFP && m >= 8)
-                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF, XFP>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
-                                   (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
+                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF, XFP, RT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+                                   s, (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
                                    (int)N, (int)K, w.biases, nullptr);
             else
-                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF>), dim3((unsigned)blocks), dim3(NW * 64), 0, s,
-                                   (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
+                hipLaunchKernelGGL((k_gemv_mfma<false, NW, F, XF, false, RT>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+                                   s, (const int8_t *)w.codes, w.scales, nullptr, nullptr, x, y, yt == RQ_F16 ? 1 : 0, m,
                                    (int)N, (int)K, w.biases, nullptr);
         }
     };
     auto go_fmt = [&](auto nwv, auto xfc) {
-        if (affine) go(nwv, std::integral_constant<int, 1>{}, xfc);
-        else go(nwv, std::integral_constant<int, 0>{}, xfc);
+        // (affine codes with f32 activations run 4 waves, see `wide`: the
+        // 8-wave variant is not built)
+        constexpr bool aff_ok = decltype(nwv)::value == 4 || !decltype(xfc)::value;
+        if (affine) {
+            if constexpr (aff_ok) go(nwv, std::integral_constant<int, 1>{}, xfc, std::integral_constant<int, 1>{});
+        }
+        else if (two) go(nwv, std::integral_constant<int, 0>{}, std::false_type{}, std::integral_constant<int, 2>{});
+        else go(nwv, std::integral_constant<int, 0>{}, xfc, std::integral_constant<int, 1>{});
     };
     auto go_x = [&](auto nwv) {
         if (xf) go_fmt(nwv, std::true_type{});
@@ -506,7 +565,7 @@ static int launch_mfma(const rq_qweight &w, const rq_qweight *w2, const void *x,
     // affine codes (m = 16 7.9 -> 8.4).
     // affine codes with f32 activations hold four scale and bias vectors per
     // batch: at 8 waves (256 VGPRs each) they spill, at 4 they fit
-    const bool wide = K <= 4096 && blocks <= 512 && !(affine && xf);
+    const bool wide = K <= 4096 && blocks1 <= 512 && !(affine && xf);
     if (wide) go_x(std::integral_constant<int, 8>{});
     else go_x(std::integral_constant<int, 4>{});
     RQ_LAUNCH_CHECK();

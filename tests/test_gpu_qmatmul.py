@@ -114,6 +114,20 @@ def test_gemv_tall_weights(ctx, engine, n, k):
     assert ok, (max_abs, rel)
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 4100, 1024), (5, 8184, 2048), (16, 8200, 1024), (12, 8216, 4096),
+                                   (16, 11008, 4096)])
+def test_gemv_row_tile_pairs(ctx, engine, m, n, k):
+    # 3 <= m <= 16 with 257-512 row tiles of 16 (or more than 512 at m > 8)
+    # runs two tiles per block: 4100 and 8200 leave the last block's second
+    # tile empty, 8184 and 8216 leave a part-filled last tile
+    g = synth.rng(n * 31 + m)
+    q, s = synth.rowwise_weight(g, n, k)
+    x = synth.activations(g, m, k)
+    y = qmm(ctx, engine, QuantizedTensor.rowwise(ctx, q, s), x, np.float16)
+    max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(q, s, None, x.astype(np.float32), 0))
+    assert ok, (max_abs, rel)
+
+
 # m = 1-2: the dot2 GEMV; 3-16: the matrix-core GEMV in blocks of 64 rows over k slices
 # (136 rows: three row blocks, the last ragged; k = 11008 is 43 batches of 256, sliced unevenly)
 @pytest.mark.parametrize("k", [1024, 4096, 11008])

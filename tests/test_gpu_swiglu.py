@@ -57,6 +57,21 @@ def test_swiglu_small(ctx, engine, m):
     assert ok
 
 
+@pytest.mark.parametrize("m,inter", [(4, 8196), (12, 8204)])
+def test_swiglu_row_tile_pairs(ctx, engine, m, inter):
+    # 1025-1026 gate/up row tiles of 8 run two tiles per block: 8196 leaves the
+    # last block's second tile empty, 8204 part-filled.  y in f32: K = 8196
+    # puts |y| past the fp16 range at these statistics
+    g = synth.rng(inter + m)
+    wg, sg, wu, su, wd, sd = weights(g, inter, 1024)
+    x = synth.activations(g, m, 1024)
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
+    _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
+    assert ok_h, "intermediate h"
+    max_abs, rel, ok = f16_tol_check(y, orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32)))
+    assert ok, (max_abs, rel)
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_config3_swiglu_7b(ctx, engine, m):
     # configs[2] statistics (X ~ N(0,1), scales up to 0.02, K = 11008) put |y|
