@@ -21,6 +21,14 @@
 //    expansion work: 2048x4096x11008 178.8 -> 172.6 us, m = 768 and 1024 at
 //    N = K = 4096 (128x128 tile, against 4 waves) 38.3 -> 35.5 us and
 //    42.9 -> 40.6 us; 2048x4096x4096 unchanged.
+//    The 128x64 and 64x64 tiles run 4 waves as two k-groups of 2 (2 x 1
+//    along features), each wave all the tile's tokens x 32 features (KSPLIT_M:
+//    the groups finish alternate token tiles): every expanded W fragment then
+//    feeds 2 (64x64) or 4 (128x64) MFMAs instead of 1 or 2.  At these tiles
+//    the int8 expansion, not the MFMAs, had set the pace (a timing-only copy
+//    without it ran 512x2048x5632 24.2 -> 17.4 us): 512x2048x5632 24.2 ->
+//    ~20.0, 512x2048x2048 10.7 -> 8.6, 256x4096x4096 18.7 -> 14.5,
+//    64x4096x4096 (split K) 9.5 -> 8.5, 512x4096x11008 (128x64) 63 -> 57 us.
 //  * Staging is direct-to-LDS DMA (buffer_load_dwordx4 ... lds): each wave
 //    moves 1 KiB units from global memory straight into LDS, so tiles never
 //    pass through VGPRs or ds_write (register staging measured ~10% slower,
@@ -167,7 +175,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     constexpr int K16 = 4 / KG;    // 16-k slices per wave per stage
     constexpr int WGM = WPG / WGN; // wave grid: WGM along tokens, WGN along features
     constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
-    static_assert(KG == 1 || (KG == 2 && FN % 2 == 0), "two k-groups split the finishing work by feature tiles");
+    // The two k-groups finish disjoint halves of the wave tile: the feature
+    // tiles i % 2 == kg, or (KSPLIT_M, a wave tile one feature tile wide) the
+    // token tiles j % 2 == kg.
+    constexpr bool KSPLIT_M = KG == 2 && FN % 2 != 0;
+    static_assert(KG == 1 || (KG == 2 && (FN % 2 == 0 || FM % 2 == 0)), "two k-groups split the finishing work");
     // W2: the weight is staged two k-steps at a time (128-byte row pieces, whole
     // cache lines) in a ring of two pairs beside an S-stage X ring.
     static_assert(!W2 || (KG == 2 && PINGPONG && S == 4), "W pairs: two k-groups, ping-pong, 4 X stages");
@@ -200,6 +212,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     const int kg = wave / WPG, wq = wave % WPG;
     const int wm = wq / WGN, wn = wq % WGN;
     const int fr = lane % 32, h = lane / 32;
+    // whether this wave finishes output tile (i, j) of its wave tile
+    auto mine = [&](int i, int j) { return KG == 1 || (KSPLIT_M ? j % 2 == kg : i % 2 == kg); };
     const int nk_all = K / 64, ks = (nk_all + splits - 1) / splits;
     const int k0 = split * ks, nk = min(ks, nk_all - k0);  // this block's k-steps [k0, k0 + nk)
 
@@ -287,11 +301,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // The per-feature scales of the outputs this wave finishes (feature tile i
-    // = KG io + kg, features fl + r of each 8-row group g), requested before
-    // the k loop: loaded by the epilogue, they cost a round trip on every
-    // block's tail.  Past the weight's rows: a valid row, zeroed at use.
-    constexpr int FNO = FN / KG;
-    auto feat = [&](int io, int g) { return wn * TN + (KG * io + kg) * 32 + 8 * g + h * 4; };
+    // = FKG io + (kg, or 0 with KSPLIT_M), features fl + r of each 8-row group
+    // g), requested before the k loop: loaded by the epilogue, they cost a
+    // round trip on every block's tail.  Past the weight's rows: a valid row,
+    // zeroed at use.
+    constexpr int FKG = KSPLIT_M ? 1 : KG;   // feature-tile stride of the finished tiles
+    constexpr int FNO = FN / FKG;            // feature tiles this wave finishes
+    constexpr int FMO = KSPLIT_M ? FM / 2 : FM;  // token tiles this wave finishes of each
+    auto feat = [&](int io, int g) { return wn * TN + (FKG * io + (KSPLIT_M ? 0 : kg)) * 32 + 8 * g + h * 4; };
     auto wrow = [&](int fl) { return nw0 + (PAIR && fl >= HB ? fl - HB : fl); };
     float esc[FNO][4][4];
     if constexpr (FMT == 0) {
@@ -471,8 +488,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     // two k-groups: the step's MFMAs first, its DMA after them,
                     // so no wave queues behind the block's DMA burst before
                     // reaching its MFMAs (the ring leaves the DMA S - 1 steps
-                    // to land): 1-3 % faster at 256x128 and 128x128, 2 %
-                    // slower with one group at 128x64
+                    // to land): 1-3 % faster at 256x128 and 128x128, and at
+                    // the two-wave groups of 128x64 and 64x64 (512x2048x5632
+                    // 21.0 -> 19.8 us, 64x4096x4096 9.2 -> 8.6); 2 % slower
+                    // with one group of 4 waves at 128x64
                     fetch((u + 1) % S, kt + u + 1, f[(u + 1) % 2]);
                     mma(f[u % 2]);
                     dma(u % S, kt + u + S);
@@ -501,40 +520,43 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     wait_vmcnt<0>();  // no DMA in flight past this point
 
     if constexpr (KG == 2) {
-        // Group g finishes the feature tiles i with i % 2 == g: it hands its
+        // Group g finishes its half of the wave tile (see mine): it hands its
         // partial sums of the other tiles to the other group through the
         // (now idle) ring, lane-contiguous 16-byte pieces, and adds the other
         // group's partials of its own tiles.
-        constexpr int HF = FN / 2;  // feature tiles per group
-        static_assert(2 * WPG * HF * FM * 16 * 64 * 4 <= RING, "exchange does not fit");
+        constexpr int HT = FN * FM / 2;  // tiles each group finishes
+        static_assert(2 * WPG * HT * 16 * 64 * 4 <= RING, "exchange does not fit");
         float4 *xch = reinterpret_cast<float4 *>(&ring[0]);
-        // slot of (target group, wave position, tile pair (i / 2, j), quad r4), then lane
-        auto slot = [&](int tg, int ih, int j, int r4) { return (((tg * WPG + wq) * HF + ih) * FM + j) * 4 + r4; };
+        // index of tile (i, j) among the half it belongs to (the same in both groups)
+        auto hidx = [&](int i, int j) { return KSPLIT_M ? i * (FM / 2) + j / 2 : (i / 2) * FM + j; };
+        // slot of (target group, wave position, tile, quad r4), then lane
+        auto slot = [&](int tg, int ti, int r4) { return ((tg * WPG + wq) * HT + ti) * 4 + r4; };
         __syncthreads();  // every wave is done with the ring
 #pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            if (i % 2 == kg) continue;
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-            for (int j = 0; j < FM; ++j)
+            for (int j = 0; j < FM; ++j) {
+                if (mine(i, j)) continue;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4)
-                    xch[slot(1 - kg, i / 2, j, r4) * 64 + lane] =
+                    xch[slot(1 - kg, hidx(i, j), r4) * 64 + lane] =
                         make_float4(acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]);
-        }
+            }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
-            if (i % 2 != kg) continue;
 #pragma unroll
-            for (int j = 0; j < FM; ++j)
+            for (int j = 0; j < FM; ++j) {
+                if (!mine(i, j)) continue;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
-                    const float4 o = xch[slot(kg, i / 2, j, r4) * 64 + lane];
+                    const float4 o = xch[slot(kg, hidx(i, j), r4) * 64 + lane];
                     acc[i][j][4 * r4] += o.x;
                     acc[i][j][4 * r4 + 1] += o.y;
                     acc[i][j][4 * r4 + 2] += o.z;
                     acc[i][j][4 * r4 + 3] += o.w;
                 }
+            }
         }
     }
 
@@ -568,18 +590,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     // scope there are no other writes to publish and no stale lines to read.
     if constexpr (BM == 64 && BN == 64) {  // only the 64x64 grids split (see launch_tiled)
         if (splits > 1) {
-            constexpr int FNO = FN / KG;  // feature tiles this wave finishes
+            constexpr int FT = FNO * FMO;  // tiles this wave finishes
             const size_t slot_floats = (size_t)BM * BN;
+            // finished tile (i, jj) of this wave, in (feature, token) order
+            auto fidx = [&](int i, int jj) { return (i / FKG) * FMO + (KSPLIT_M ? jj / 2 : jj); };
             auto piece = [&](int i, int jj, int r4) {
-                return ((((wave * FNO + i / KG) * FM + jj) * 4 + r4) * 64 + lane) * 16u;
+                return (((wave * FT + fidx(i, jj)) * 4 + r4) * 64 + lane) * 16u;
             };
             {
                 const auto rs = make_rsrc(skw + ((size_t)tile * splits + split) * slot_floats, (uint32_t)slot_floats * 4u);
 #pragma unroll
                 for (int i = 0; i < FN; ++i) {
-                    if (KG == 2 && i % 2 != kg) continue;
 #pragma unroll
-                    for (int jj = 0; jj < FM; ++jj)
+                    for (int jj = 0; jj < FM; ++jj) {
+                        if (!mine(i, jj)) continue;
 #pragma unroll
                         for (int r4 = 0; r4 < 4; ++r4) {
                             // whole vectors: a bit_cast of an ext-vector element reads element 0
@@ -588,6 +612,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, piece(i, jj, r4),
                                                                    0, 16);
                         }
+                    }
                 }
             }
             wait_vmcnt<0>();  // this thread's pieces have landed
@@ -607,7 +632,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                     for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
             // UNR splits per round trip (their pieces loaded together, ~64
             // VGPRs), added in split order
-            constexpr int PIECES = FNO * FM * 4, UNR = PIECES >= 16 ? 1 : 16 / PIECES;
+            constexpr int PIECES = FT * 4, UNR = PIECES >= 16 ? 1 : 16 / PIECES;
             auto rsrc_of = [&](int sp) {
                 return make_rsrc(skw + ((size_t)tile * splits + sp) * slot_floats, (uint32_t)slot_floats * 4u);
             };
@@ -617,32 +642,32 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
                     const auto rs = rsrc_of(min(sp0 + u, splits - 1));
-                    int p = 0;
+                    // (piece index from fidx, not a running count: a count past
+                    // the runtime-skipped tiles would index v dynamically)
 #pragma unroll
-                    for (int i = 0; i < FN; ++i) {
-                        if (KG == 2 && i % 2 != kg) continue;
+                    for (int i = 0; i < FN; ++i)
 #pragma unroll
-                        for (int jj = 0; jj < FM; ++jj)
+                        for (int jj = 0; jj < FM; ++jj) {
+                            if (!mine(i, jj)) continue;
 #pragma unroll
-                            for (int r4 = 0; r4 < 4; ++r4, ++p)
-                                v[u][p] = __builtin_bit_cast(
+                            for (int r4 = 0; r4 < 4; ++r4)
+                                v[u][fidx(i, jj) * 4 + r4] = __builtin_bit_cast(
                                     floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, piece(i, jj, r4), 0, 16));
-                    }
+                        }
                 }
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
                     if (sp0 + u >= splits) break;
-                    int p = 0;
 #pragma unroll
-                    for (int i = 0; i < FN; ++i) {
-                        if (KG == 2 && i % 2 != kg) continue;
+                    for (int i = 0; i < FN; ++i)
 #pragma unroll
-                        for (int jj = 0; jj < FM; ++jj)
+                        for (int jj = 0; jj < FM; ++jj) {
+                            if (!mine(i, jj)) continue;
 #pragma unroll
-                            for (int r4 = 0; r4 < 4; ++r4, ++p)
+                            for (int r4 = 0; r4 < 4; ++r4)
 #pragma unroll
-                                for (int e = 0; e < 4; ++e) acc[i][jj][4 * r4 + e] += v[u][p][e];
-                    }
+                                for (int e = 0; e < 4; ++e) acc[i][jj][4 * r4 + e] += v[u][fidx(i, jj) * 4 + r4][e];
+                        }
                 }
             }
         }
@@ -664,8 +689,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         __syncthreads();  // every wave is done with the ring (and the k-group exchange)
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
-            if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
-            const int io = i / KG;
+            if (!KSPLIT_M && !mine(i, 0)) continue;  // the other k-group finishes this tile
+            const int io = i / FKG;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int fl = feat(io, g);  // feature within the tile
@@ -675,6 +700,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                 for (int r = 0; r < 4; ++r) sc[r] = wr + r < NL ? (FMT == 0 ? esc[io][g][r] : 1.0f) : 0.0f;
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
+                    if (!mine(i, j)) continue;
                     uint8_t *dst = ot + (wm * TM + j * 32 + fr) * RS + fl * EB;
                     const float tf = tfac[j];
                     const float v0 = acc[i][j][4 * g] * sc[0] * tf, v1 = acc[i][j][4 * g + 1] * sc[1] * tf;
@@ -765,8 +791,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         }
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
-            if (KG == 2 && i % 2 != kg) continue;  // the other k-group finishes this tile
-            const int io = i / KG;
+            if (!KSPLIT_M && !mine(i, 0)) continue;  // the other k-group finishes this tile
+            const int io = i / FKG;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int nb = n0 + feat(io, g);  // weight row
@@ -776,7 +802,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     const int mm = m0 + wm * TM + j * 32 + fr;
-                    if (mm >= M) continue;
+                    if (!mine(i, j) || mm >= M) continue;
                     float v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] * sc[r] * tfac[j];
@@ -979,8 +1005,10 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
     // Groups of 4 token panels per XCD and the ping-pong fragments beat
     // token-major order and single buffering by 5-15 % at m = 2048.  The two
     // large tiles run two k-groups of 4 waves with the weight staged in pairs
-    // of k-steps; at 128x64 and 64x64 one group of 4 waves measured 2-4 %
-    // faster.  128x256 rather than 256x128: for the same outputs per block
+    // of k-steps; 128x64 and 64x64 two k-groups of 2 waves, each wave all the
+    // tile's tokens (two groups of 4 waves there, each wave still expanding
+    // its W fragment for 1-2 MFMAs, measured 2-4 % slower than one group of 4
+    // and than these).  128x256 rather than 256x128: for the same outputs per block
     // (one 128x64 wave tile per wave) it stages 32 KiB per k-step instead of
     // 40, in 256 cache lines instead of 320 (2048x4096x4096 64.5 -> 62.1 us,
     // N = 11008 176.4 -> 171.2, K = 11008 162.5 -> 156.9 us in one run), and
@@ -1003,8 +1031,8 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
         return launch_tiled<128, 128, true, 4, 8, 2, 2, true>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr,
                                                               xscale);
     if (fills(128, 64))
-        return launch_tiled<128, 64, true, 6, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
-    return launch_tiled<64, 64, true, 4, 4, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
+        return launch_tiled<128, 64, true, 6, 4, 2, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
+    return launch_tiled<64, 64, true, 4, 4, 2, 2>(w, scales, fmt, x, y, yt, m, 4, cus, ws, s, np, nullptr, xscale);
 }
 
 }  // namespace
@@ -1042,8 +1070,8 @@ int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, cons
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     if (tile_fills(m, N, cus, 128, 256) || tile_fills(m, N, cus, 128, 128)) return RQ_ERR_UNSUPPORTED;
     if (tile_fills(m, N, cus, 128, 64))
-        return launch_tiled<128, 64, true, 6, 4, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
-    return launch_tiled<64, 64, true, 4, 4, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+        return launch_tiled<128, 64, true, 6, 4, 2, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+    return launch_tiled<64, 64, true, 4, 4, 2, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
 }
 
 int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
