@@ -944,8 +944,11 @@ __device__ __forceinline__ float dpp_f(float v) {
 // (exact).  Any finite row fits fp16 that way, small rows keep fp16's full
 // precision, and a row whose values all lie in fp16's normal range gives the
 // same products as a plain conversion (scaling by a power of two commutes
-// with rounding there).  The row is read twice (its maximum, then the
-// conversion; the second read hits L2), K % 8 == 0.
+// with rounding there).  K % 8 == 0.  NI > 0 (K <= NI * 2048): each thread
+// holds its NI 8-value chunks in registers from the maximum to the
+// conversion, so the row is read once; NI == 0 reads it twice (the second
+// read hits L2).
+template <int NI>
 __global__ __launch_bounds__(256) void k_cast_f16_rows(const float *__restrict__ x, _Float16 *__restrict__ y,
                                                        float *__restrict__ rs, int K) {
     __shared__ float wmax[4];
@@ -953,11 +956,23 @@ __global__ __launch_bounds__(256) void k_cast_f16_rows(const float *__restrict__
     const float4 *xr = reinterpret_cast<const float4 *>(x + row * K);
     half8 *yr = reinterpret_cast<half8 *>(y + row * K);
     const int n8 = K / 8, t = threadIdx.x, lane = t & 63;
+    auto amax8 = [](float4 a, float4 b) {
+        return fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    };
     float amax = 0.0f;
-    for (int i = t; i < n8; i += 256) {
-        const float4 a = xr[2 * i], b = xr[2 * i + 1];
-        amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+    float4 va[NI > 0 ? NI : 1], vb[NI > 0 ? NI : 1];
+    if constexpr (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {  // every load in flight before the first use
+            const int i = t + 256 * j;
+            va[j] = i < n8 ? xr[2 * i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vb[j] = i < n8 ? xr[2 * i + 1] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) amax = fmaxf(amax, amax8(va[j], vb[j]));
+    } else {
+        for (int i = t; i < n8; i += 256) amax = fmaxf(amax, amax8(xr[2 * i], xr[2 * i + 1]));
     }
     amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
     amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
@@ -973,13 +988,20 @@ __global__ __launch_bounds__(256) void k_cast_f16_rows(const float *__restrict__
     // amax = f * 2^E, f in [0.5, 1); a zero, infinite or NaN maximum gives
     // E = 0 (an inf or NaN stays one)
     const int e = max(__builtin_amdgcn_frexp_expf(amax) - 15, -126);
-    for (int i = t; i < n8; i += 256) {
-        const float4 a = xr[2 * i], b = xr[2 * i + 1];
-        const half8 h = {(_Float16)__builtin_amdgcn_ldexpf(a.x, -e), (_Float16)__builtin_amdgcn_ldexpf(a.y, -e),
-                         (_Float16)__builtin_amdgcn_ldexpf(a.z, -e), (_Float16)__builtin_amdgcn_ldexpf(a.w, -e),
-                         (_Float16)__builtin_amdgcn_ldexpf(b.x, -e), (_Float16)__builtin_amdgcn_ldexpf(b.y, -e),
-                         (_Float16)__builtin_amdgcn_ldexpf(b.z, -e), (_Float16)__builtin_amdgcn_ldexpf(b.w, -e)};
-        yr[i] = h;
+    auto cvt = [e](float4 a, float4 b) {
+        return half8{(_Float16)__builtin_amdgcn_ldexpf(a.x, -e), (_Float16)__builtin_amdgcn_ldexpf(a.y, -e),
+                     (_Float16)__builtin_amdgcn_ldexpf(a.z, -e), (_Float16)__builtin_amdgcn_ldexpf(a.w, -e),
+                     (_Float16)__builtin_amdgcn_ldexpf(b.x, -e), (_Float16)__builtin_amdgcn_ldexpf(b.y, -e),
+                     (_Float16)__builtin_amdgcn_ldexpf(b.z, -e), (_Float16)__builtin_amdgcn_ldexpf(b.w, -e)};
+    };
+    if constexpr (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int i = t + 256 * j;
+            if (i < n8) yr[i] = cvt(va[j], vb[j]);
+        }
+    } else {
+        for (int i = t; i < n8; i += 256) yr[i] = cvt(xr[2 * i], xr[2 * i + 1]);
     }
     if (t == 0) rs[row] = __builtin_amdgcn_ldexpf(1.0f, e);
 }
@@ -1130,8 +1152,13 @@ int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dty
     const size_t eb = yt == RQ_F16 ? 2 : 4;
     for (int64_t r0 = 0; r0 < m; r0 += chunk) {
         const int64_t mc = std::min(chunk, m - r0);
-        hipLaunchKernelGGL(k_cast_f16_rows, dim3((unsigned)mc), dim3(256), 0, s, static_cast<const float *>(x) + r0 * K,
-                           x16, xs, (int)K);
+        const float *xc = static_cast<const float *>(x) + r0 * K;
+        const int64_t per = cdiv(K / 8, 256);  // 8-value chunks per thread
+        if (per <= 1) hipLaunchKernelGGL(k_cast_f16_rows<1>, dim3((unsigned)mc), dim3(256), 0, s, xc, x16, xs, (int)K);
+        else if (per <= 2) hipLaunchKernelGGL(k_cast_f16_rows<2>, dim3((unsigned)mc), dim3(256), 0, s, xc, x16, xs, (int)K);
+        else if (per <= 4) hipLaunchKernelGGL(k_cast_f16_rows<4>, dim3((unsigned)mc), dim3(256), 0, s, xc, x16, xs, (int)K);
+        else if (per <= 8) hipLaunchKernelGGL(k_cast_f16_rows<8>, dim3((unsigned)mc), dim3(256), 0, s, xc, x16, xs, (int)K);
+        else hipLaunchKernelGGL(k_cast_f16_rows<0>, dim3((unsigned)mc), dim3(256), 0, s, xc, x16, xs, (int)K);
         RQ_LAUNCH_CHECK();
         const int st = gemm_tiles(w, scales, fmt, x16, static_cast<uint8_t *>(y) + (size_t)r0 * (size_t)N * eb, yt, mc,
                                   cus, ws, s, GemmPair{}, xs);

@@ -492,6 +492,8 @@ def test_gemm_f32_activations_past_fp16_range(ctx, engine, m, n, k, fmt):
     (770, 4096, 128, 1, 64, np.float32),    # 128x128 pairs
     (1500, 4100, 1088, 1, 64, np.float16),  # 128x256 pairs, odd k-step count
     (1500, 4100, 1024, 0, 0, np.float32),   # rowwise, f32 activations
+    (300, 512, 6144, 0, 0, np.float32),     # f32 rows cast from 4 chunks per thread
+    (130, 256, 20480, 0, 0, np.float32),    # f32 rows too long to hold: read twice
     (3000, 256, 16384, 0, 0, np.float32),   # two chunks
     (3000, 256, 16384, 1, 64, np.float32),  # two chunks, affine
 ])
