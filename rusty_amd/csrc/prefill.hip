@@ -69,19 +69,32 @@ __global__ __launch_bounds__(NT) void k_add_rmsnorm_rows(float *__restrict__ x, 
     const int t = threadIdx.x, h4 = H / 4;
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)blockIdx.x * H);
     const float4 *yr = y ? reinterpret_cast<const float4 *>(y + (size_t)blockIdx.x * H) : nullptr;
-    float4 v[NV];
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    const half4 *w4 = reinterpret_cast<const half4 *>(nw);
+    // every load of the row -- x, y and the norm weight -- requested before the
+    // first use: one memory round trip (the weight had been a second one, after
+    // the reduction)
+    float4 v[NV], a[NV];
+    half4 w[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = t + NT * j;
+        if (i < h4) {
+            v[j] = xr[i];
+            if (y) a[j] = yr[i];
+            if (nw) w[j] = w4[i];
+        }
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int i = t + NT * j;
         if (i >= h4) break;
-        v[j] = xr[i];
         if (y) {
-            const float4 a = yr[i];
-            v[j].x += a.x;
-            v[j].y += a.y;
-            v[j].z += a.z;
-            v[j].w += a.w;
+            v[j].x += a[j].x;
+            v[j].y += a[j].y;
+            v[j].z += a[j].z;
+            v[j].w += a[j].w;
             xr[i] = v[j];
         }
         ss = fmaf(v[j].x, v[j].x, fmaf(v[j].y, v[j].y, fmaf(v[j].z, v[j].z, fmaf(v[j].w, v[j].w, ss))));
@@ -93,16 +106,13 @@ __global__ __launch_bounds__(NT) void k_add_rmsnorm_rows(float *__restrict__ x, 
     __syncthreads();
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    const half4 *w4 = reinterpret_cast<const half4 *>(nw);
     half4 *o4 = reinterpret_cast<half4 *>(xn + (size_t)blockIdx.x * H);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int i = t + NT * j;
         if (i >= h4) break;
-        const half4 w = w4[i];
-        const half4 r = {(_Float16)((v[j].x * inv) * (float)w.x), (_Float16)((v[j].y * inv) * (float)w.y),
-                         (_Float16)((v[j].z * inv) * (float)w.z), (_Float16)((v[j].w * inv) * (float)w.w)};
+        const half4 r = {(_Float16)((v[j].x * inv) * (float)w[j].x), (_Float16)((v[j].y * inv) * (float)w[j].y),
+                         (_Float16)((v[j].z * inv) * (float)w[j].z), (_Float16)((v[j].w * inv) * (float)w[j].w)};
         o4[i] = r;
     }
 }
