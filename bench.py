@@ -474,7 +474,8 @@ def _lora_workspace(m, k, n, rank):
 
 def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False,
                 affine_group: int = 0) -> dict:
-    """1.1B int8 Llama greedy decode, one HIP-graph launch per token.
+    """1.1B int8 Llama greedy decode, from captured HIP graphs (four
+    steps per launch, the runner's default).
     Algorithmic bytes per token = int8 codes + f32 scales of every Linear and
     the lm_head + the fp16 KV cache rows attention reads (positions 0..pos,
     once per KV head) + one fp16 embedding row.  With ``affine_group`` every
@@ -790,7 +791,7 @@ def main() -> int:
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
                          "the power limit; diagnostic only")
     ap.add_argument("--decode-eager", action="store_true",
-                    help="decode steps as direct launches instead of one graph per token (for tools that "
+                    help="decode steps as direct launches instead of graph replays (for tools that "
                          "do not trace graphs)")
     args = ap.parse_args()
 

@@ -347,12 +347,15 @@ int rq_llama_prefill(rq_llama *model, const int32_t *tokens, int32_t n, rq_strea
 int rq_llama_set_prefill(rq_llama *model, int32_t rows);
 /* n_steps greedy decode steps, each feeding the previous token.  The
  * sequence grows by n_steps; fails with RQ_ERR_SHAPE past max_seq cached
- * positions.  Asynchronous (graph launches only).  In graph mode the first
- * step of the runner's life captures and instantiates the step graph on
- * `stream` (stream capture, no device work) before launching it. */
+ * positions.  Asynchronous (graph launches only).  In graph mode a run
+ * replays a graph of four consecutive steps for each full four and a
+ * one-step graph for the rest; the first run that needs either captures and
+ * instantiates it on `stream` (stream capture, no device work) before
+ * launching it. */
 int rq_llama_decode(rq_llama *model, int32_t n_steps, rq_stream stream);
-/* Steps run as one graph launch each (default, use_graph = 1) or as direct
- * kernel launches on the stream (0: for tools that do not trace graphs). */
+/* Steps run as graph launches (default, use_graph = 1: four steps or one
+ * per launch) or as direct kernel launches on the stream (0: for tools that
+ * do not trace graphs). */
 int rq_llama_set_graph(rq_llama *model, int use_graph);
 /* Copies up to `capacity` tokens of the sequence (prompt, then generated) to
  * host memory and stores the sequence length in *length.  Synchronizes. */

@@ -6,9 +6,9 @@ attention with RoPE and a KV cache -> residual add -> RMSNorm -> SwiGLU MLP ->
 residual add, lib.rs:364-378), final RMSNorm and the lm_head projection, with
 greedy (top-1) sampling.  Every Linear is a quantized weight read by the
 fused dequant-GEMV (per-row int8, or the reference's affine u8 codes as an
-MLX checkpoint holds them: ``load_mlx``); the whole step runs as one HIP
-graph on the device (librusty_hip.so), with no host round trip between
-tokens.
+MLX checkpoint holds them: ``load_mlx``); the whole step runs from captured
+HIP graphs on the device (librusty_hip.so; four steps per graph launch where
+a run has four), with no host round trip between tokens.
 
 The reference has no decode loop (its LlamaModel::forward takes the ids and a
 KV cache but nothing drives generation); the loop defined here is: prefill the
@@ -234,7 +234,7 @@ def load_mlx(model_dir, max_seq: int | None = None) -> tuple[LlamaConfig, LlamaH
 
 
 class LlamaRunner:
-    """Device-resident model + KV cache + captured step graph."""
+    """Device-resident model + KV cache + captured step graphs."""
 
     def __init__(self, ctx: WgpuContext, cfg: LlamaConfig, weights: LlamaHostWeights):
         self.ctx, self.cfg = ctx, cfg

@@ -187,6 +187,30 @@ def test_step_graph_captured_at_first_graph_step(ctx):
     check_steps(TINY, w, tb, lb, 20, 1e-2, "lazy graph")
 
 
+def test_multi_step_graph_matches_single_steps(ctx):
+    """Runs of at least four steps replay a graph that holds four consecutive
+    steps (the rest of the run: the one-step graph): decoding 11 steps in one
+    call (4 + 4 + 1 + 1 + 1), then 5 more (4 + 1), gives the tokens and final
+    logits, bit for bit, of the same steps as direct launches one at a time."""
+    w = synth_weights(TINY, seed=31)
+    prompt = np.random.default_rng(32).integers(0, TINY.vocab, 17)
+    a = LlamaRunner(ctx, TINY, w)
+    a.prefill(prompt)
+    a.decode(11)
+    a.decode(5)
+    ta, la = a.tokens(), a.logits()
+    a.close()
+    b = LlamaRunner(ctx, TINY, w)
+    b.set_graph(False)
+    b.prefill(prompt)
+    for _ in range(16):
+        b.decode(1)
+    tb, lb = b.tokens(), b.logits()
+    b.close()
+    np.testing.assert_array_equal(ta, tb)
+    np.testing.assert_array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
 def test_invalid_arguments(ctx):
     w = synth_weights(TINY, seed=23)
     r = LlamaRunner(ctx, TINY, w)
