@@ -108,7 +108,8 @@ def test_c_client_runs(tmp_path):
 
 
 def test_integration_binding_lists_every_entry_point():
-    """INTEGRATION.md's Rust `extern "C"` block declares exactly the header's functions."""
+    """The integration guide's Rust `extern "C"` block (the binding a maintainer
+    adds on the reference side) declares exactly the header's functions."""
     import re
     from pathlib import Path
 
