@@ -536,6 +536,8 @@ def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eag
                       f"{prompt_len}-token random prompt, {steps} greedy steps timed, best of {reps}",
             "weights": (f"affine u8, f32 scale + bias per {affine_group} (the reference's format)" if affine_group
                         else "per-row int8, f32 scale per row"),
+            "launch": ("direct kernel launches" if eager else
+                       "captured step graphs: four steps per graph launch, a one-step graph for the rest"),
             "generated_head": [int(t) for t in toks[prompt_len:prompt_len + 8]],
             "prefill": {"tok_s": round(prompt_len / (best_pf * 1e-3), 1), "ms": round(best_pf, 3),
                         "tflops": round(pf_flops / (best_pf * 1e-3) / 1e12, 1),
