@@ -146,7 +146,8 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int gm,
 // k-step's values for the block's BN features are contiguous: each wave
 // stages 64 of them per k-step (one 4-byte DMA per lane) beside its X stage,
 // and the weight is expanded to fp16 u*s + b while the fragments are read.
-// PAIR, SwiGLU's gate and up (per-row codes, n_split = I rows each, N = 2 I):
+// PAIR, SwiGLU's gate and up (n_split = I rows each, N = 2 I; affine codes
+// stage their scales from the gate's table and the up weight's, scalesb):
 // tile column block tn covers rows [j0, j0 + BN/2) of both weights, j0 =
 // tn * BN/2 -- the gate (W, scales) in tile columns [0, BN/2), the up weight
 // (Wb, scalesb) in [BN/2, BN) -- and the epilogue writes h = silu(g) * u
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
                                                      int *__restrict__ skc, int group, const uint8_t *__restrict__ Wb,
                                                      const float *__restrict__ scalesb, int n_split, RopeOut ro,
                                                      const float *__restrict__ xscale) {
-    static_assert(!ROPE || (BN == 64 && FMT == 0 && !PAIR), "rotary epilogue: one 64-wide head per tile");
+    static_assert(!ROPE || (BN == 64 && !PAIR), "rotary epilogue: one 64-wide head per tile");
     // KG k-groups of NW/KG waves: group g takes k16 slices [g*K16, (g+1)*K16)
     // of every 64-k stage, so a wave tile covers KG times the outputs for the
     // same fragment bytes; the groups' partial sums meet in LDS at the end.
@@ -229,13 +230,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
     const auto rwb = PAIR ? make_rsrc_s(Wb + (size_t)nw0 * K, (uint32_t)min(HB, NL - nw0) * (uint32_t)K) : rw;
     // affine: lane l of wave w stages value i = 64 w + l of [s | c] for the
     // block's features (rows past N and lanes past 2 BN read zero); the
-    // transposed scales hold 2 N floats per group
+    // transposed scales hold 2 NL floats per group.  PAIR: the features of
+    // the tile's second half are up rows, whose table is scalesb; 64 divides
+    // HB, so each wave's 64 values come from one table (the DMA's buffer
+    // descriptor is wave-uniform).
     const int gstep = FMT == 1 ? group / 64 : 1;  // k-steps per scale group
-    const auto rsc = make_rsrc(scales, FMT == 1 ? (uint32_t)(K / group) * (uint32_t)N * 8u : 0u);
+    const bool up_w = PAIR && ((wave * 64) % BN) >= HB;  // wave-uniform
+    const auto rsc = make_rsrc(up_w ? static_cast<const float *>(scalesb) : scales,
+                               FMT == 1 ? (uint32_t)(K / group) * (uint32_t)NL * 8u : 0u);
     uint32_t scoff = kOOB;
     if constexpr (FMT == 1) {
-        const int i = wave * 64 + lane, n = n0 + (i < BN ? i : i - BN);
-        if (i < 2 * BN && n < N) scoff = (uint32_t)((i < BN ? 0 : N) + n) * 4u;
+        const int i = wave * 64 + lane, f = i < BN ? i : i - BN;
+        const int n = nw0 + (up_w ? f - HB : f);  // row of its weight (PAIR: of the gate or the up weight)
+        if (i < 2 * BN && n < NL) scoff = (uint32_t)((i < BN ? 0 : NL) + n) * 4u;
     }
 
     // Source offsets (k = 0) of this lane in each of the wave's DMA units,
@@ -270,7 +277,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rowwise(const uint8_t *__restr
         const uint32_t sx = ring_lds + (uint32_t)stage * (uint32_t)XSTRIDE;
         if constexpr (FMT == 1)
             dma4(rsc, ring_lds + (uint32_t)(RING_X + stage * SCB + wave * 256),
-                 live && scoff != kOOB ? scoff + (uint32_t)(kt / gstep) * (uint32_t)N * 8u : kOOB);
+                 live && scoff != kOOB ? scoff + (uint32_t)(kt / gstep) * (uint32_t)NL * 8u : kOOB);
 #pragma unroll
         for (int q = 0; q < XUW; ++q) dma16(rx, sx + (uint32_t)(wave * XUW + q) * 1024u, live ? xoff[q] + kt * 128 : kOOB);
         if constexpr (!W2) {
@@ -872,12 +879,16 @@ int launch_tiled(const rq_qweight &w, const float *scales, int fmt, const void *
     };
     if constexpr (BN == 64 && !PAIR) {
         if (rope) {
-            go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, false, true>);
+            if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1, false, true>);
+            else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, false, true>);
             RQ_LAUNCH_CHECK();
             return RQ_OK;
         }
     }
-    if constexpr (PAIR) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, true>);
+    if constexpr (PAIR) {
+        if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1, true>);
+        else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0, true>);
+    }
     else if (fmt == 1) go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 1>);
     else go(k_gemm_rowwise<BM, BN, PINGPONG, S, NW, WGN, KG, W2, 0>);
     RQ_LAUNCH_CHECK();
@@ -1072,34 +1083,45 @@ int gemm_tiles(const rq_qweight &w, const float *scales, int fmt, const void *x,
 // the same rows of both, so the tile heuristic sees the combined width (at 512
 // tokens x 5632 features: 128x256 tiles over both instead of two launches of
 // 128x128 tiles that each leave a third of the CUs idle) and g and u never
-// leave the block.  Per-row int8 weights of one shape, fp16 activations,
-// I % 8 == 0; RQ_ERR_UNSUPPORTED otherwise, or when the grid is too small for
-// the two large tiles.
+// leave the block.  Weights of one shape, per-row int8 or affine u8 with
+// their load-time tables (rq_qweight_prepare, the same group), fp16
+// activations, I % 8 == 0; RQ_ERR_UNSUPPORTED otherwise, or when the grid is
+// too small for the two large tiles.
 // A Llama layer's packed q/k/v projection with the rotary epilogue (see
 // k_gemm_rowwise, ROPE): q fp16 [m][n_heads][64] to q, k and v into the
-// caches at positions ro.p0 .. ro.p0 + m - 1.  Per-row int8 weights of
-// (n_heads + 2 n_kv) 64 rows, fp16 x, and a token count whose tile choice is
-// 64 wide (64x64 or 128x64); RQ_ERR_UNSUPPORTED (nothing launched) otherwise,
+// caches at positions ro.p0 .. ro.p0 + m - 1.  Weights of (n_heads + 2 n_kv)
+// 64 rows, per-row int8 or affine u8 with the load-time table
+// (rq_qweight_prepare), fp16 x, and a token count whose tile choice is 64
+// wide (64x64 or 128x64); RQ_ERR_UNSUPPORTED (nothing launched) otherwise,
 // and the caller runs the product and the rotation separately.
 int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, const RopeOut &ro, _Float16 *q,
                          int num_cus, const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;
-    if (w.format != RQ_Q_ROWWISE_I8 || K % 64 != 0 || K > (1 << 21) || m < 1 || m > 0x7fffffff ||
+    const bool affine = w.format == RQ_Q_AFFINE_U8;
+    if (affine && !(w.prep && affine_prep_bytes(w) > 0)) return RQ_ERR_UNSUPPORTED;
+    if ((!affine && w.format != RQ_Q_ROWWISE_I8) || K % 64 != 0 || K > (1 << 21) || m < 1 || m > 0x7fffffff ||
         N != (int64_t)(ro.n_heads + 2 * ro.n_kv) * 64 || !ro.rope || !ro.kc || !ro.vc || !aligned(w.codes, 16) ||
         !aligned(x, 16) || !aligned(q, 8) || !aligned(ro.kc, 8) || !aligned(ro.vc, 8) || !aligned(ro.rope, 16) ||
         (int64_t)ro.p0 + m > ro.max_seq)
         return RQ_ERR_UNSUPPORTED;
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     if (tile_fills(m, N, cus, 128, 256) || tile_fills(m, N, cus, 128, 128)) return RQ_ERR_UNSUPPORTED;
+    const float *sc = affine ? w.prep : w.scales;
+    const int fmt = affine ? 1 : 0;
     if (tile_fills(m, N, cus, 128, 64))
-        return launch_tiled<128, 64, true, 6, 4, 2, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
-    return launch_tiled<64, 64, true, 4, 4, 2, 2>(w, w.scales, 0, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+        return launch_tiled<128, 64, true, 6, 4, 2, 2>(w, sc, fmt, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
+    return launch_tiled<64, 64, true, 4, 4, 2, 2>(w, sc, fmt, x, q, RQ_F16, m, 4, cus, ws, s, GemmPair{}, &ro);
 }
 
 int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void *x, rq_dtype xt, void *h, int64_t m,
                        int num_cus, const GemmWorkspace &ws, hipStream_t s) {
     const int64_t I = gate.n_out, K = gate.k_in;
-    if (gate.format != RQ_Q_ROWWISE_I8 || up.format != RQ_Q_ROWWISE_I8 || up.n_out != I || up.k_in != K ||
+    // affine codes: both weights with their load-time tables (rq_qweight_prepare), the same group
+    const bool affine = gate.format == RQ_Q_AFFINE_U8;
+    if (affine && (up.format != RQ_Q_AFFINE_U8 || up.group != gate.group || !gate.prep || !up.prep ||
+                   affine_prep_bytes(gate) == 0 || affine_prep_bytes(up) == 0))
+        return RQ_ERR_UNSUPPORTED;
+    if ((!affine && (gate.format != RQ_Q_ROWWISE_I8 || up.format != RQ_Q_ROWWISE_I8)) || up.n_out != I || up.k_in != K ||
         xt != RQ_F16 || I % 8 != 0 || K % 64 != 0 || K > (1 << 21) || !aligned(gate.codes, 16) ||
         !aligned(up.codes, 16) || !aligned(x, 16) || !aligned(h, 16) || m > 0x7fffffff || 2 * I > 0x7fffffff ||
         128 * I * 2 >= (1ll << 31))
@@ -1108,9 +1130,10 @@ int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void 
     w.n_out = 2 * I;
     GemmPair pair;
     pair.w = static_cast<const uint8_t *>(up.codes);
-    pair.scales = up.scales;
+    pair.scales = affine ? up.prep : up.scales;
     pair.n_split = I;
-    return gemm_tiles(w, gate.scales, 0, x, h, RQ_F16, m, num_cus > 0 ? num_cus : 256, ws, s, pair);
+    return gemm_tiles(w, affine ? gate.prep : gate.scales, affine ? 1 : 0, x, h, RQ_F16, m, num_cus > 0 ? num_cus : 256,
+                      ws, s, pair);
 }
 
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,

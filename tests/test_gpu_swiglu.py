@@ -131,6 +131,39 @@ def test_swiglu_prefill_fused(ctx, engine, m, inter, hidden):
     assert ok
 
 
+@pytest.mark.parametrize("m,inter,hidden", [(1000, 2760, 1024), (768, 2816, 1024)], ids=["128x256", "128x128"])
+def test_swiglu_prefill_fused_affine(ctx, engine, m, inter, hidden):
+    """The fused gate/up GEMM on the reference's affine u8 weights (scale tables
+    prepared at load): the tile's gate half stages its scales and offsets from
+    the gate's table, the up half from the up weight's.  2760 rows leave the
+    last 128x256 tile a partial half per weight.  h (against g and u rounded to
+    fp16, as the kernel rounds them) and y on sampled rows against the f64
+    truth."""
+    g = synth.rng(1500 + m)
+    ug, sg, bg = synth.affine_weight(g, inter, hidden)
+    uu, su, bu = synth.affine_weight(g, inter, hidden)
+    ud, sd, bd = synth.affine_weight(g, hidden, inter)
+    G, U, D = (QuantizedTensor.affine(ctx, *a) for a in ((ug, sg, bg), (uu, su, bu), (ud, sd, bd)))
+    x = synth.activations(g, m, hidden, sigma=0.5)
+    X = UnifiedTensor.new(ctx, x, dtype=DType.FP16)
+    Y = UnifiedTensor.new(ctx, np.full((m, hidden), np.nan, np.float32), dtype=DType.FP32)
+    h = engine.mlp_swiglu(ctx, X, G, U, D, Y)
+    rows = np.unique(np.concatenate([[0, 1, m // 2, m - 2, m - 1], synth.rng(m).integers(0, m, 12)]))
+    xr = x[rows].astype(np.float32)
+    gt = orc.qlinear_truth(ug, sg, bg, xr, 1).astype(np.float16).astype(np.float64)
+    ut = orc.qlinear_truth(uu, su, bu, xr, 1).astype(np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):
+        ht = gt / (1.0 + np.exp(-gt)) * ut
+    hd = h.to_vec().reshape(-1)[: m * inter].reshape(m, inter)[rows]
+    max_abs, rel, ok_h = f16_tol_check(hd, ht)
+    print(f"[fused affine {m}x{inter}x{hidden}] h max_abs={max_abs:.3e}", flush=True)
+    assert ok_h
+    truth = orc.qlinear_truth(ud, sd, bd, ht.astype(np.float16).astype(np.float32), 1)
+    max_abs, rel, ok = f16_tol_check(Y.to_vec().reshape(m, hidden)[rows], truth)
+    print(f"[fused affine {m}x{inter}x{hidden}] y max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    assert ok
+
+
 def test_swiglu_prefill_fused_128x128(ctx, engine):
     """1024 tokens x 2 x 2048 rows take the fused epilogue on the 128x128 tile
     (the cases above run 128x256): h and y against the f64 truth on rows at
