@@ -445,6 +445,10 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_mfma(const int8_t *__restrict
         } else {
             mma(A);
         }
+    } else {
+        // no batch for this wave (nb <= wave: K <= 256 wave), which may still
+        // finish a row tile below (wave t finishes tile t): its scales all the same
+        load_scales();
     }
 
     // acct[t] = D[feature 4 q + r][token fr] of tile t, partial over this

@@ -115,11 +115,13 @@ def test_gemv_tall_weights(ctx, engine, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 4100, 1024), (5, 8184, 2048), (16, 8200, 1024), (12, 8216, 4096),
-                                   (16, 11008, 4096)])
+                                   (16, 11008, 4096), (8, 4100, 64), (5, 5000, 256), (12, 8200, 128)])
 def test_gemv_row_tile_pairs(ctx, engine, m, n, k):
     # 3 <= m <= 16 with 257-512 row tiles of 16 (or more than 512 at m > 8)
     # runs two tiles per block: 4100 and 8200 leave the last block's second
-    # tile empty, 8184 and 8216 leave a part-filled last tile
+    # tile empty, 8184 and 8216 leave a part-filled last tile.  k <= 256 is
+    # one 256-k batch: the wave that finishes the second tile has none of its
+    # own (its row scales were once left unloaded)
     g = synth.rng(n * 31 + m)
     q, s = synth.rowwise_weight(g, n, k)
     x = synth.activations(g, m, k)

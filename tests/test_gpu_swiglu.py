@@ -57,14 +57,15 @@ def test_swiglu_small(ctx, engine, m):
     assert ok
 
 
-@pytest.mark.parametrize("m,inter", [(4, 8196), (12, 8204)])
-def test_swiglu_row_tile_pairs(ctx, engine, m, inter):
+@pytest.mark.parametrize("m,inter,hidden", [(4, 8196, 1024), (12, 8204, 1024), (8, 5632, 256)])
+def test_swiglu_row_tile_pairs(ctx, engine, m, inter, hidden):
     # 1025-1026 gate/up row tiles of 8 run two tiles per block: 8196 leaves the
-    # last block's second tile empty, 8204 part-filled.  y in f32: K = 8196
-    # puts |y| past the fp16 range at these statistics
+    # last block's second tile empty, 8204 part-filled; hidden 256 is one
+    # 256-k batch, none for the wave that finishes the second tile.  y in f32:
+    # K = 8196 puts |y| past the fp16 range at these statistics
     g = synth.rng(inter + m)
-    wg, sg, wu, su, wd, sd = weights(g, inter, 1024)
-    x = synth.activations(g, m, 1024)
+    wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
+    x = synth.activations(g, m, hidden)
     y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
     _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
     assert ok_h, "intermediate h"
