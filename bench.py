@@ -455,21 +455,24 @@ def ops_bench(ctx, engine, use_graph: bool = True) -> list:
     for m in (1, 512):
         x = UnifiedTensor.new(ctx, synth.activations(g, m, 4096), dtype=DType.FP16)
         y = UnifiedTensor.empty(ctx, [m, 4096], DType.FP16)
-        need = _lora_workspace(m, 4096, 4096, rank)
+        need = max(_lora_workspace(m, 4096, 4096, rank, tree) for tree in (False, True))
         ws = UnifiedTensor.empty(ctx, [need], DType.U8)
         us = timed(lambda: [engine.qmatmul_lora(ctx, x, w, la, lb, y, ws) for _ in range(4)], 4)
+        us_tree = timed(lambda: [engine.qmatmul_lora(ctx, x, w, la, lb, y, ws, tree=True) for _ in range(4)], 4)
         base = timed(lambda: [engine.qmatmul(ctx, x, w, y) for _ in range(4)], 4)
         out.append({"op": "qmatmul_lora", "ref": "rusty-graph/src/lib.rs:69-83", "m": m, "n_out": 4096, "k_in": 4096,
-                    "rank": rank, "us": round(us, 2), "us_without_adapter": round(base, 2),
+                    "rank": rank, "us": round(us, 2), "us_tree": round(us_tree, 2), "us_without_adapter": round(base, 2),
                     "adapter_chain_floor_us": round(chain_floor(4096), 2),
-                    "what": "y fp16 = x . deq(W)^T + (x . A) . B; the same weight every call (L2/MALL-resident)"})
+                    "what": "y fp16 = x . deq(W)^T + (x . A) . B; the same weight every call (L2/MALL-resident); "
+                            "us: x . A in the reference's k-ascending chain (its bits), us_tree: as a fixed-order "
+                            "reduction tree (RQ_LORA_TREE, f32 rounding of the same product)"})
     return out
 
 
-def _lora_workspace(m, k, n, rank):
+def _lora_workspace(m, k, n, rank, tree=False):
     from rusty_amd import _lib
 
-    return int(_lib.lib().rq_qmatmul_lora_workspace(m, k, n, rank, 1, 1))
+    return int(_lib.lib().rq_qmatmul_lora_ex_workspace(m, k, n, rank, 1, 1, _lib.RQ_LORA_TREE if tree else 0))
 
 
 def decode_loop(ctx, prompt_len: int = 512, steps: int = 128, reps: int = 2, eager: bool = False,

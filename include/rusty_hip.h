@@ -238,6 +238,23 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
                     const float *lora_b, int64_t rank, void *y, rq_dtype y_dtype, int64_t m, void *workspace,
                     size_t workspace_bytes, rq_stream stream);
 
+/* rq_qmatmul_lora with a choice of adapter arithmetic (no counterpart in the
+ * reference, whose only arithmetic is the chain; for callers that want the
+ * adapter at decode sizes without its latency).  flags 0: exactly
+ * rq_qmatmul_lora.  RQ_LORA_TREE (adapters of rank 1..64): X.A as a
+ * reduction tree -- slices of 256 k, a fixed-order sum inside each slice, the
+ * slices added in order -- deterministic and within f32 rounding of the
+ * exact product, but not the reference's bit pattern; wider adapters keep
+ * the chain.  The k_in-step fma chain per output that reproduces the
+ * reference's bits is latency-bound (~16 us at k_in = 4096, whatever m).
+ * workspace: at least rq_qmatmul_lora_ex_workspace(..., flags) bytes. */
+#define RQ_LORA_TREE 1u
+size_t rq_qmatmul_lora_ex_workspace(int64_t m, int64_t k_in, int64_t n_out, int64_t rank, rq_dtype x_dtype,
+                                    rq_dtype y_dtype, unsigned flags);
+int rq_qmatmul_lora_ex(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, const float *lora_a,
+                       const float *lora_b, int64_t rank, void *y, rq_dtype y_dtype, int64_t m, unsigned flags,
+                       void *workspace, size_t workspace_bytes, rq_stream stream);
+
 /* MLP::forward (rusty-graph/src/lib.rs:317-323):
  * y = down( silu(x . gate^T) * (x . up^T) ), silu(v) = v / (1 + exp(-v))
  * (kernels.wgsl:104-113; the elementwise product kernels.wgsl:146-151).

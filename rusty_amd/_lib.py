@@ -28,6 +28,7 @@ RQ_F16 = 1
 RQ_Q_ROWWISE_I8 = 0
 RQ_Q_AFFINE_U8 = 1
 RQ_AFFINE_FMA = 1
+RQ_LORA_TREE = 1
 
 
 class rq_qweight(ctypes.Structure):
@@ -122,13 +123,17 @@ _SIGNATURES = {
     "rq_qmatmul_lora_workspace": [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int],
     "rq_qmatmul_lora": [_P, POINTER(rq_qweight), _P, c_int, _P, _P, ctypes.c_int64, _P, c_int, ctypes.c_int64, _P,
                         c_size_t, _P],
+    "rq_qmatmul_lora_ex_workspace": [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int,
+                                     c_uint32],
+    "rq_qmatmul_lora_ex": [_P, POINTER(rq_qweight), _P, c_int, _P, _P, ctypes.c_int64, _P, c_int, ctypes.c_int64,
+                           c_uint32, _P, c_size_t, _P],
     "rq_llama_set_graph": [_P, c_int],
     "rq_llama_set_prefill": [_P, c_int32],
     "rq_llama_tokens": [_P, POINTER(c_int32), c_int32, POINTER(c_int32), _P],
     "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }
 _RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p, "rq_qmatmul_lora_workspace": c_size_t,
-             "rq_qweight_prep_bytes": c_size_t}
+             "rq_qmatmul_lora_ex_workspace": c_size_t, "rq_qweight_prep_bytes": c_size_t}
 
 
 class RqError(RuntimeError):

@@ -325,10 +325,13 @@ class ComputeEngine:
 
     def qmatmul_lora(self, ctx: WgpuContext, x: UnifiedTensor, w: QuantizedTensor, lora_a: UnifiedTensor,
                      lora_b: UnifiedTensor, out: UnifiedTensor, workspace: UnifiedTensor | None = None,
-                     stream=None) -> None:
+                     stream=None, tree: bool = False) -> None:
         """``Linear::forward`` with a LoRA adapter (rusty-graph/src/lib.rs:69-83):
         ``out = x . deq(w)^T + (x . A) . B``, A f32 [k_in, rank], B f32
-        [rank, n_out], unscaled as the reference adds it."""
+        [rank, n_out], unscaled as the reference adds it.  ``tree``: x . A as
+        a fixed-order reduction tree (rq_qmatmul_lora_ex, RQ_LORA_TREE) instead
+        of the reference's k-ascending chain -- within f32 rounding of it, not
+        its bits, and without the chain's k_in-step latency."""
         if x.dtype not in _XDT or out.dtype not in _XDT:
             raise ValueError("x and out must be FP16 or FP32")
         if lora_a.dtype is not DType.FP32 or lora_b.dtype is not DType.FP32:
@@ -339,12 +342,20 @@ class ComputeEngine:
                 or lora_b.numel != rank * w.n_out:
             raise ValueError(f"x {x.shape} / A {lora_a.shape} / B {lora_b.shape} / out {out.shape} do not match "
                              f"weight [{w.n_out}, {w.k_in}]")
-        need = _lib.lib().rq_qmatmul_lora_workspace(m, w.k_in, w.n_out, rank, _XDT[x.dtype], _XDT[out.dtype])
+        flags = _lib.RQ_LORA_TREE if tree else 0
+        need = _lib.lib().rq_qmatmul_lora_ex_workspace(m, w.k_in, w.n_out, rank, _XDT[x.dtype], _XDT[out.dtype],
+                                                       flags)
         if workspace is None:
             workspace = UnifiedTensor.empty(ctx, [max(need, 1)], DType.U8)
         d = w.descriptor()
-        call("rq_qmatmul_lora", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], lora_a.ptr, lora_b.ptr, rank,
-             out.ptr, _XDT[out.dtype], m, workspace.ptr, workspace.numel * workspace.dtype.itemsize, _stream(stream))
+        if tree:
+            call("rq_qmatmul_lora_ex", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], lora_a.ptr, lora_b.ptr,
+                 rank, out.ptr, _XDT[out.dtype], m, flags, workspace.ptr, workspace.numel * workspace.dtype.itemsize,
+                 _stream(stream))
+        else:
+            call("rq_qmatmul_lora", ctx.handle, ctypes.byref(d), x.ptr, _XDT[x.dtype], lora_a.ptr, lora_b.ptr, rank,
+                 out.ptr, _XDT[out.dtype], m, workspace.ptr, workspace.numel * workspace.dtype.itemsize,
+                 _stream(stream))
 
     def qmatmul_dx(self, ctx: WgpuContext, dy: UnifiedTensor, w: QuantizedTensor, dx: UnifiedTensor,
                    stream=None) -> None:
