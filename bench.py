@@ -446,8 +446,17 @@ def ops_bench(ctx, engine, use_graph: bool = True) -> list:
     dx = UnifiedTensor.empty(ctx, [m, 4096], DType.FP32)
     us = timed(lambda: [engine.qmatmul_dx(ctx, dy, w, dx) for _ in range(4)], 4)
     gf = 2 * m * 4096 * 4096 / us / 1e3
+    w.dx_table(ctx)  # built once per weight, outside the timed calls
+    dws = UnifiedTensor.empty(ctx, [int(_lib.lib().rq_qmatmul_dx_mfma_workspace(m, 4096))], DType.U8)
+    us_mfma = timed(lambda: [engine.qmatmul_dx(ctx, dy, w, dx, mfma=True, workspace=dws) for _ in range(4)], 4)
+    gf_mfma = 2 * m * 4096 * 4096 / us_mfma / 1e3
     out.append({"op": "qmatmul_dx", "ref": "rusty-autograd/src/lib.rs:152-158", "m": m, "n_out": 4096, "k_in": 4096,
-                "us": round(us, 2), "gflops": round(gf, 1), "frac_fp32_peak": round(gf / 1e3 / FP32_PEAK_TFLOPS, 4)})
+                "us": round(us, 2), "gflops": round(gf, 1), "frac_fp32_peak": round(gf / 1e3 / FP32_PEAK_TFLOPS, 4),
+                "us_mfma": round(us_mfma, 2), "gflops_mfma": round(gf_mfma, 1),
+                "frac_fp16_peak_mfma": round(2 * gf_mfma / 1e3 / FP16_MFMA_PEAK_TFLOPS, 4),
+                "what": "us: f32 fma chain in ascending n_out (the reference's bits); us_mfma: rq_qmatmul_dx_mfma, "
+                        "dY . s split into two fp16 halves against the transposed codes (twice the MFMA work of "
+                        "one fp16 product; frac_fp16_peak_mfma counts both halves)"})
 
     rank = 16
     la = UnifiedTensor.new(ctx, (g.standard_normal((4096, rank)) * 0.01).astype(np.float32))

@@ -295,6 +295,28 @@ int rq_mlp_swiglu_noalloc(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight 
 int rq_qmatmul_dx(rq_ctx *ctx, const rq_qweight *w, const void *dy, rq_dtype dy_dtype, void *dx, rq_dtype dx_dtype,
                   int64_t m, rq_stream stream);
 
+/* The same input gradient on the matrix cores, for per-row int8 weights (no
+ * counterpart in the reference, whose only arithmetic is the f32 chain; for
+ * fine-tuning loops that run it every step).  A table built once per weight
+ * holds the codes transposed, so that the reduction over n_out is contiguous
+ * for the matrix cores, written twice side by side, and k_in unit scales:
+ * rq_qweight_dx_table_bytes(w) bytes (0: the weight is not served -- per-row
+ * int8 codes, 16-byte aligned, n_out a multiple of 32, k_in of 16),
+ * 256-byte aligned, filled by rq_qweight_dx_table.  rq_qmatmul_dx_mfma then
+ * forms v = dY . s per row (f32), splits it into two fp16 halves under a
+ * per-row power of two (any finite row; hi + lo = v to ~2^-22 relative) and
+ * runs the prefill GEMM over both halves against the table: exact products,
+ * f32 sums -- the f32 bar against the exact product, not rq_qmatmul_dx's bit
+ * pattern.  workspace: rq_qmatmul_dx_mfma_workspace(m, n_out) bytes,
+ * 256-byte aligned.  dX fp16 needs 8-byte, f32 16-byte alignment.  Uses the
+ * context's GEMM workspace as rq_qmatmul does. */
+size_t rq_qweight_dx_table_bytes(const rq_qweight *w);
+int rq_qweight_dx_table(rq_ctx *ctx, const rq_qweight *w, void *table, size_t table_bytes, rq_stream stream);
+size_t rq_qmatmul_dx_mfma_workspace(int64_t m, int64_t n_out);
+int rq_qmatmul_dx_mfma(rq_ctx *ctx, const rq_qweight *w, const void *table, const void *dy, rq_dtype dy_dtype,
+                       void *dx, rq_dtype dx_dtype, int64_t m, void *workspace, size_t workspace_bytes,
+                       rq_stream stream);
+
 /* ---- int8-weight Llama greedy decode ------------------------------------
  * LlamaModel::forward (rusty-graph/src/lib.rs:420-436) over LlamaBlock
  * (:364-378: norm1 -> Attention -> add -> norm2 -> MLP -> add), Attention

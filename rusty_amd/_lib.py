@@ -116,6 +116,10 @@ _SIGNATURES = {
     "rq_mlp_swiglu_noalloc": [_P, POINTER(rq_qweight), POINTER(rq_qweight), POINTER(rq_qweight), _P, c_int, _P,
                               c_int, c_int64, _P],
     "rq_qmatmul_dx": [_P, POINTER(rq_qweight), _P, c_int, _P, c_int, c_int64, _P],
+    "rq_qweight_dx_table_bytes": [POINTER(rq_qweight)],
+    "rq_qweight_dx_table": [_P, POINTER(rq_qweight), _P, c_size_t, _P],
+    "rq_qmatmul_dx_mfma_workspace": [c_int64, c_int64],
+    "rq_qmatmul_dx_mfma": [_P, POINTER(rq_qweight), _P, _P, c_int, _P, c_int, c_int64, _P, c_size_t, _P],
     "rq_llama_create": [_P, POINTER(rq_llama_config), POINTER(rq_llama_weights), POINTER(c_void_p)],
     "rq_llama_destroy": [_P],
     "rq_llama_prefill": [_P, POINTER(c_int32), c_int32, _P],
@@ -133,7 +137,8 @@ _SIGNATURES = {
     "rq_llama_logits": [_P, POINTER(ctypes.c_float), _P],
 }
 _RESTYPES = {"rq_status_string": c_char_p, "rq_last_error": c_char_p, "rq_qmatmul_lora_workspace": c_size_t,
-             "rq_qmatmul_lora_ex_workspace": c_size_t, "rq_qweight_prep_bytes": c_size_t}
+             "rq_qmatmul_lora_ex_workspace": c_size_t, "rq_qweight_prep_bytes": c_size_t,
+             "rq_qweight_dx_table_bytes": c_size_t, "rq_qmatmul_dx_mfma_workspace": c_size_t}
 
 
 class RqError(RuntimeError):

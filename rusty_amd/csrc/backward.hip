@@ -22,6 +22,7 @@
 // overlap its arithmetic (a few blocks per CU at prompt-sized m cannot hide
 // the latency by occupancy alone: 512 x 4096 x 4096 took 730 us with
 // single-buffered 16-step tiles).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -195,3 +196,185 @@ int launch_qmatmul_dx(const rq_qweight &w, const void *dy, rq_dtype dyt, void *d
 }
 
 }  // namespace rq
+
+// ---- Input gradient on the matrix cores (per-row int8 codes) ----
+//
+// dX[m][k] = sum_n dY[m][n] s[n] q[n][k] is a GEMM whose reduction runs along
+// n_out, while the int8 rows of W are contiguous along k_in: the matrix cores
+// need the reduction contiguous in each lane's operand.  So a table built once
+// per weight (load time, rq_qweight_dx_table) holds the codes transposed and
+// written twice side by side, qt[k][j] = q[j mod n][k] for j < 2 n_out, and
+// k_in unit scales; each dY row becomes v = dY s (f32, one rounding) scaled by
+// the power of two 2^-e that puts max |v| in [2^14, 2^15), then two fp16
+// halves x2[m] = [fp16(v 2^-e) | fp16(v 2^-e - hi)] (hi + lo = v 2^-e to
+// ~2^-22 relative).  The prefill GEMM (gemm.hip) then computes
+// dX[m][k] = 2^e sum_j x2[m][j] qt[k][j]: exact fp16 x int8 products, f32
+// sums -- the f32 bar against the exact product, not the chain's bit pattern
+// (rq_qmatmul_dx keeps that).  Memory: the table is 2 B per weight element.
+namespace rq {
+namespace {
+
+constexpr int TT = 64;  // transpose tile, bytes per side
+
+// qt[k][j] = qt[k][j + n] = q[j][k], one 64 x 64 tile per block; n % 16 == 0,
+// k % 16 == 0, so every 16-byte piece lies wholly inside or outside.
+__global__ __launch_bounds__(256) void k_dx_transpose(const uint8_t *__restrict__ q, uint8_t *__restrict__ qt,
+                                                      int64_t n, int64_t k) {
+    __shared__ uint8_t tile[TT][TT + 4];  // [n local][k local]
+    const int t = threadIdx.x, r = t / 4, c = (t % 4) * 16;
+    const int64_t n0 = (int64_t)blockIdx.y * TT, k0 = (int64_t)blockIdx.x * TT;
+    {
+        const int64_t gn = n0 + r, gk = k0 + c;
+        const uint4 v = gn < n && gk < k ? *reinterpret_cast<const uint4 *>(q + gn * k + gk) : make_uint4(0, 0, 0, 0);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tile[r][c + e] = (uint8_t)(wd[e / 4] >> (8 * (e % 4)));
+    }
+    __syncthreads();
+    const int64_t gk = k0 + r, gn = n0 + c;  // row gk of qt, its bytes gn .. gn + 15
+    if (gk < k && gn < n) {
+        uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) wd[e / 4] |= (uint32_t)tile[c + e][r] << (8 * (e % 4));
+        const uint4 v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        *reinterpret_cast<uint4 *>(qt + gk * 2 * n + gn) = v;
+        *reinterpret_cast<uint4 *>(qt + gk * 2 * n + n + gn) = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fill_ones(float *__restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 1.0f;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Row i of dY (one block): v[j] = dY[i][j] s[j]; the row maximum (DPP steps
+// and one barrier), 2^e with max |v| 2^-e in [2^14, 2^15) (e >= -126: 2^e
+// stays a normal f32; a zero row gives e = 0), then x2[i][j] = hi,
+// x2[i][n + j] = lo and xs[i] = 2^e.  The row is read twice (the second time
+// from L2).
+template <bool DYF16>
+__global__ __launch_bounds__(256) void k_dx_split(const void *__restrict__ dy, const float *__restrict__ s,
+                                                  _Float16 *__restrict__ x2, float *__restrict__ xs, int64_t n) {
+    __shared__ float wmax[4];
+    const int64_t row = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63;
+    auto v_at = [&](int64_t j) {
+        const float d = DYF16 ? (float)static_cast<const _Float16 *>(dy)[row * n + j]
+                              : static_cast<const float *>(dy)[row * n + j];
+        return d * s[j];
+    };
+    float amax = 0.0f;
+    for (int64_t j = t; j < n; j += 256) amax = fmaxf(amax, fabsf(v_at(j)));
+    amax = fmaxf(amax, dppf<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dppf<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dppf<0x141>(amax));  // row_half_mirror
+    amax = fmaxf(amax, dppf<0x140>(amax));  // row_mirror: each 16-lane row holds its maximum
+    const auto rl = [](float v, int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    };
+    amax = fmaxf(fmaxf(rl(amax, 0), rl(amax, 16)), fmaxf(rl(amax, 32), rl(amax, 48)));
+    if (lane == 0) wmax[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int e = max(__builtin_amdgcn_frexp_expf(amax) - 15, -126);
+    _Float16 *xr = x2 + row * 2 * n;
+    for (int64_t j = t; j < n; j += 256) {
+        const float v = __builtin_amdgcn_ldexpf(v_at(j), -e);
+        const _Float16 hi = (_Float16)v;
+        xr[j] = hi;
+        xr[n + j] = (_Float16)(v - (float)hi);
+    }
+    if (t == 0) xs[row] = __builtin_amdgcn_ldexpf(1.0f, e);
+}
+
+bool dx_table_ok(const rq_qweight &w) {
+    return w.format == RQ_Q_ROWWISE_I8 && w.n_out >= 32 && w.n_out % 32 == 0 && w.k_in >= 16 && w.k_in % 16 == 0 &&
+           2 * w.n_out <= (1 << 21) && w.k_in <= 0x7fffffff && aligned(w.codes, 16);
+}
+size_t dx_codes_bytes(const rq_qweight &w) { return ((size_t)2 * w.n_out * w.k_in + 255) & ~size_t(255); }
+
+}  // namespace
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" {
+
+size_t rq_qweight_dx_table_bytes(const rq_qweight *w) {
+    if (!w || check_qweight(w) != RQ_OK || !dx_table_ok(*w)) return 0;
+    return dx_codes_bytes(*w) + (size_t)w->k_in * 4;
+}
+
+int rq_qweight_dx_table(rq_ctx *ctx, const rq_qweight *w, void *table, size_t table_bytes, rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    if (!dx_table_ok(*w))
+        return fail(RQ_ERR_UNSUPPORTED, "the matrix-core input gradient takes per-row int8 codes, 16-byte aligned, "
+                                        "n_out a multiple of 32, k_in a multiple of 16");
+    const size_t need = rq_qweight_dx_table_bytes(w);
+    if (!table || table_bytes < need || !aligned(table, 256))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "table of %zu bytes (256-byte aligned), %zu needed", table_bytes, need);
+    hipStream_t s = pick(ctx, stream);
+    const int64_t n = w->n_out, k = w->k_in;
+    if (cdiv(k, TT) > 0x7fffffff || cdiv(n, TT) > 65535) return fail(RQ_ERR_SHAPE, "weight too large to transpose");
+    uint8_t *qt = static_cast<uint8_t *>(table);
+    hipLaunchKernelGGL(k_dx_transpose, dim3((unsigned)cdiv(k, TT), (unsigned)cdiv(n, TT)), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(w->codes), qt, n, k);
+    RQ_LAUNCH_CHECK();
+    float *ones = reinterpret_cast<float *>(qt + dx_codes_bytes(*w));
+    hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)std::min<int64_t>(cdiv(k, 256), 4096)), dim3(256), 0, s, ones, k);
+    RQ_LAUNCH_CHECK();
+    return RQ_OK;
+}
+
+size_t rq_qmatmul_dx_mfma_workspace(int64_t m, int64_t n_out) {
+    if (m < 0 || n_out < 0) return 0;
+    return (((size_t)m * (size_t)n_out * 4 + 255) & ~size_t(255)) + (size_t)m * 4;
+}
+
+int rq_qmatmul_dx_mfma(rq_ctx *ctx, const rq_qweight *w, const void *table, const void *dy, rq_dtype dy_dtype,
+                       void *dx, rq_dtype dx_dtype, int64_t m, void *workspace, size_t workspace_bytes,
+                       rq_stream stream) {
+    RQ_ENTER(ctx);
+    int st = check_qweight(w);
+    if (st != RQ_OK) return st;
+    if ((dy_dtype != RQ_F16 && dy_dtype != RQ_F32) || (dx_dtype != RQ_F16 && dx_dtype != RQ_F32))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "dtype must be RQ_F16 or RQ_F32");
+    if (!dx_table_ok(*w))
+        return fail(RQ_ERR_UNSUPPORTED, "the matrix-core input gradient takes per-row int8 codes, 16-byte aligned, "
+                                        "n_out a multiple of 32, k_in a multiple of 16");
+    if (m < 0) return fail(RQ_ERR_SHAPE, "negative m");
+    int64_t t;
+    if (!mul_ok(m, w->k_in, &t) || !mul_ok(m, 2 * w->n_out, &t) || m > 0x7fffffff)
+        return fail(RQ_ERR_SHAPE, "shape overflows");
+    if (m == 0) return RQ_OK;
+    if (!dx || !dy || !table) return fail(RQ_ERR_INVALID_ARGUMENT, "null gradient or table pointer");
+    if (!aligned(table, 256)) return fail(RQ_ERR_INVALID_ARGUMENT, "table must be 256-byte aligned");
+    const size_t need = rq_qmatmul_dx_mfma_workspace(m, w->n_out);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return fail(RQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes (256-byte aligned), %zu needed",
+                    workspace_bytes, need);
+    hipStream_t s = pick(ctx, stream);
+    const int64_t n = w->n_out, k = w->k_in;
+    _Float16 *x2 = static_cast<_Float16 *>(workspace);
+    float *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + (((size_t)m * n * 4 + 255) & ~size_t(255)));
+    if (dy_dtype == RQ_F16)
+        hipLaunchKernelGGL(k_dx_split<true>, dim3((unsigned)m), dim3(256), 0, s, dy, w->scales, x2, xs, n);
+    else
+        hipLaunchKernelGGL(k_dx_split<false>, dim3((unsigned)m), dim3(256), 0, s, dy, w->scales, x2, xs, n);
+    RQ_LAUNCH_CHECK();
+    // the transposed problem: k_in rows of 2 n_out codes, unit scales
+    const uint8_t *qt = static_cast<const uint8_t *>(table);
+    const rq_qweight wt{qt, reinterpret_cast<const float *>(qt + dx_codes_bytes(*w)), nullptr, k, 2 * n,
+                        RQ_Q_ROWWISE_I8, 0, nullptr};
+    st = launch_gemm_f16_scaled(wt, wt.scales, x2, xs, dx, dx_dtype, m, ctx->num_cus, gemm_workspace(ctx, s), s);
+    if (st == RQ_ERR_UNSUPPORTED) return fail(st, "dx pointer alignment (8 bytes fp16, 16 bytes f32) not met");
+    return st;
+}
+
+}  // extern "C"

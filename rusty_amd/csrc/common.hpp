@@ -113,6 +113,11 @@ int launch_gemm_qkv_rope(const rq_qweight &w, const _Float16 *x, int64_t m, cons
                          int num_cus, const GemmWorkspace &ws, hipStream_t s);
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s);
+// Y = (xscale[row] * X[row]) . (scales * W)^T for per-row int8 W and fp16 X
+// (xscale: a power of two per activation row); RQ_ERR_UNSUPPORTED outside the
+// prefill GEMM's tiles (k_in % 64, alignment).
+int launch_gemm_f16_scaled(const rq_qweight &w, const float *scales, const _Float16 *x, const float *xscale,
+                           void *y, rq_dtype yt, int64_t m, int num_cus, const GemmWorkspace &ws, hipStream_t s);
 // Bytes of the prefill GEMM's scale table of an affine weight (0: none), and
 // the launch that builds it (table[g][0][n] = s, table[g][1][n] = b - 1024 s).
 size_t affine_prep_bytes(const rq_qweight &w);

@@ -1136,6 +1136,18 @@ int launch_gemm_swiglu(const rq_qweight &gate, const rq_qweight &up, const void 
                       ws, s, pair);
 }
 
+// Per-row int8 weight, fp16 activation rows each carrying the power of two
+// xscale[row] (the epilogue multiplies it back): the matrix-core input
+// gradient's GEMM (backward.hip).  RQ_ERR_UNSUPPORTED outside the tiles.
+int launch_gemm_f16_scaled(const rq_qweight &w, const float *scales, const _Float16 *x, const float *xscale,
+                           void *y, rq_dtype yt, int64_t m, int num_cus, const GemmWorkspace &ws, hipStream_t s) {
+    const int64_t N = w.n_out, K = w.k_in;
+    if (w.format != RQ_Q_ROWWISE_I8 || K % 64 != 0 || K > (1 << 21) || !aligned(w.codes, 16) || m > 0x7fffffff ||
+        N > 0x7fffffff || !aligned(x, 16) || (yt == RQ_F16 ? !aligned(y, 8) : !aligned(y, 16)))
+        return RQ_ERR_UNSUPPORTED;
+    return gemm_tiles(w, scales, 0, x, y, yt, m, num_cus > 0 ? num_cus : 256, ws, s, GemmPair{}, xscale);
+}
+
 int launch_gemm(const rq_qweight &w, const void *x, rq_dtype xt, void *y, rq_dtype yt, int64_t m, int num_cus,
                 const GemmWorkspace &ws, hipStream_t s) {
     const int64_t N = w.n_out, K = w.k_in;

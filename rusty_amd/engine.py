@@ -235,6 +235,20 @@ class QuantizedTensor:
         call("rq_qweight_prepare", ctx.handle, ctypes.byref(d), table.ptr, nbytes, _stream(stream))
         self.prep = table
 
+    def dx_table(self, ctx: WgpuContext, stream=None) -> "UnifiedTensor | None":
+        """The transposed-code table of the matrix-core input gradient
+        (rq_qweight_dx_table), built on first use and kept with the weight;
+        None when the weight is not served (see rq_qweight_dx_table_bytes)."""
+        if getattr(self, "_dxt", None) is None:
+            d = self.descriptor()
+            nbytes = int(_lib.lib().rq_qweight_dx_table_bytes(ctypes.byref(d)))
+            if nbytes == 0:
+                return None
+            table = UnifiedTensor.empty(ctx, [nbytes], DType.U8)
+            call("rq_qweight_dx_table", ctx.handle, ctypes.byref(d), table.ptr, nbytes, _stream(stream))
+            self._dxt = table
+        return self._dxt
+
     def descriptor(self) -> rq_qweight:
         return rq_qweight(self.codes.ptr, self.scales.ptr, self.biases.ptr if self.biases is not None else None,
                           self.n_out, self.k_in, self.format, self.group,
@@ -358,18 +372,31 @@ class ComputeEngine:
                  _stream(stream))
 
     def qmatmul_dx(self, ctx: WgpuContext, dy: UnifiedTensor, w: QuantizedTensor, dx: UnifiedTensor,
-                   stream=None) -> None:
+                   stream=None, mfma: bool = False, workspace: UnifiedTensor | None = None) -> None:
         """Input gradient of ``qmatmul`` with the weight frozen:
         ``dx[m, k_in] = dy[m, n_out] . deq(w)`` -- the ``grad_a`` of
-        ``MatMulNode::backward`` (rusty-autograd/src/lib.rs:152-158)."""
+        ``MatMulNode::backward`` (rusty-autograd/src/lib.rs:152-158).
+        ``mfma``: on the matrix cores (rq_qmatmul_dx_mfma, per-row int8
+        weights; the weight's transposed table is built on first use) -- the
+        f32 bar, not the f32 chain's bit pattern."""
         if dy.dtype not in _XDT or dx.dtype not in _XDT:
             raise ValueError("dy and dx must be FP16 or FP32")
         m = dy.numel // w.n_out if w.n_out else dx.shape[0]
         if dy.numel != m * w.n_out or dx.numel != m * w.k_in:
             raise ValueError(f"dy {dy.shape} / dx {dx.shape} do not match weight [{w.n_out}, {w.k_in}]")
         d = w.descriptor()
-        call("rq_qmatmul_dx", ctx.handle, ctypes.byref(d), dy.ptr, _XDT[dy.dtype], dx.ptr, _XDT[dx.dtype], m,
-             _stream(stream))
+        if not mfma:
+            call("rq_qmatmul_dx", ctx.handle, ctypes.byref(d), dy.ptr, _XDT[dy.dtype], dx.ptr, _XDT[dx.dtype], m,
+                 _stream(stream))
+            return
+        table = w.dx_table(ctx, stream)
+        if table is None:
+            raise ValueError(f"weight [{w.n_out}, {w.k_in}] is not served by the matrix-core input gradient")
+        need = int(_lib.lib().rq_qmatmul_dx_mfma_workspace(m, w.n_out))
+        if workspace is None:
+            workspace = UnifiedTensor.empty(ctx, [max(need, 1)], DType.U8)
+        call("rq_qmatmul_dx_mfma", ctx.handle, ctypes.byref(d), table.ptr, dy.ptr, _XDT[dy.dtype], dx.ptr,
+             _XDT[dx.dtype], m, workspace.ptr, workspace.numel * workspace.dtype.itemsize, _stream(stream))
 
     def mlp_swiglu(self, ctx: WgpuContext, x: UnifiedTensor, gate: QuantizedTensor, up: QuantizedTensor,
                    down: QuantizedTensor, out: UnifiedTensor, h: UnifiedTensor | None = None,
