@@ -251,24 +251,75 @@ __device__ __forceinline__ float dppf(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
 // Row i of dY (one block): v[j] = dY[i][j] s[j]; the row maximum (DPP steps
 // and one barrier), 2^e with max |v| 2^-e in [2^14, 2^15) (e >= -126: 2^e
 // stays a normal f32; a zero row gives e = 0), then x2[i][j] = hi,
-// x2[i][n + j] = lo and xs[i] = 2^e.  The row is read twice (the second time
-// from L2).
-template <bool DYF16>
+// x2[i][n + j] = lo and xs[i] = 2^e.  Pieces of 8 values (n % 8 == 0): with
+// VEC (dY and s 16-byte aligned) 16- or 32-byte loads, and with NI > 0
+// (n <= 2048 NI) each thread keeps its NI pieces in registers from the
+// maximum to the split, so the row is read once; otherwise it is read twice
+// (the second time from L2).
+template <bool DYF16, bool VEC, int NI>
 __global__ __launch_bounds__(256) void k_dx_split(const void *__restrict__ dy, const float *__restrict__ s,
                                                   _Float16 *__restrict__ x2, float *__restrict__ xs, int64_t n) {
     __shared__ float wmax[4];
     const int64_t row = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63;
-    auto v_at = [&](int64_t j) {
-        const float d = DYF16 ? (float)static_cast<const _Float16 *>(dy)[row * n + j]
+    const int n8 = (int)(n / 8);
+    auto piece = [&](int i, float *v) {  // v = dY[row][8i + e] * s[8i + e]
+        float sv[8], dv[8];
+        if constexpr (VEC) {
+            const float4 s0 = reinterpret_cast<const float4 *>(s)[2 * i], s1 = reinterpret_cast<const float4 *>(s)[2 * i + 1];
+            sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+            if constexpr (DYF16) {
+                const half8_t h = reinterpret_cast<const half8_t *>(static_cast<const _Float16 *>(dy) + row * n)[i];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dv[e] = (float)h[e];
+            } else {
+                const float4 *d4 = reinterpret_cast<const float4 *>(static_cast<const float *>(dy) + row * n);
+                const float4 a = d4[2 * i], b = d4[2 * i + 1];
+                dv[0] = a.x; dv[1] = a.y; dv[2] = a.z; dv[3] = a.w; dv[4] = b.x; dv[5] = b.y; dv[6] = b.z; dv[7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t j = (int64_t)8 * i + e;
+                sv[e] = s[j];
+                dv[e] = DYF16 ? (float)static_cast<const _Float16 *>(dy)[row * n + j]
                               : static_cast<const float *>(dy)[row * n + j];
-        return d * s[j];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = dv[e] * sv[e];
+    };
+    auto amax8 = [](const float *v) {
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
+        return a;
     };
     float amax = 0.0f;
-    for (int64_t j = t; j < n; j += 256) amax = fmaxf(amax, fabsf(v_at(j)));
+    float held[NI > 0 ? NI : 1][8];
+    if constexpr (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {  // every load in flight before the first use
+            const int i = t + 256 * j;
+            if (i < n8) piece(i, held[j]);
+            else
+#pragma unroll
+                for (int e = 0; e < 8; ++e) held[j][e] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) amax = fmaxf(amax, amax8(held[j]));
+    } else {
+        for (int i = t; i < n8; i += 256) {
+            float v[8];
+            piece(i, v);
+            amax = fmaxf(amax, amax8(v));
+        }
+    }
     amax = fmaxf(amax, dppf<0xB1>(amax));   // quad_perm [1,0,3,2]
     amax = fmaxf(amax, dppf<0x4E>(amax));   // quad_perm [2,3,0,1]
     amax = fmaxf(amax, dppf<0x141>(amax));  // row_half_mirror
@@ -281,12 +332,30 @@ __global__ __launch_bounds__(256) void k_dx_split(const void *__restrict__ dy, c
     __syncthreads();
     amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     const int e = max(__builtin_amdgcn_frexp_expf(amax) - 15, -126);
-    _Float16 *xr = x2 + row * 2 * n;
-    for (int64_t j = t; j < n; j += 256) {
-        const float v = __builtin_amdgcn_ldexpf(v_at(j), -e);
-        const _Float16 hi = (_Float16)v;
-        xr[j] = hi;
-        xr[n + j] = (_Float16)(v - (float)hi);
+    half8_t *hr = reinterpret_cast<half8_t *>(x2 + row * 2 * n);
+    auto split = [&](int i, const float *v) {
+        half8_t hi, lo;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float w = __builtin_amdgcn_ldexpf(v[q], -e);
+            hi[q] = (_Float16)w;
+            lo[q] = (_Float16)(w - (float)hi[q]);
+        }
+        hr[i] = hi;
+        hr[n8 + i] = lo;
+    };
+    if constexpr (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int i = t + 256 * j;
+            if (i < n8) split(i, held[j]);
+        }
+    } else {
+        for (int i = t; i < n8; i += 256) {
+            float v[8];
+            piece(i, v);
+            split(i, v);
+        }
     }
     if (t == 0) xs[row] = __builtin_amdgcn_ldexpf(1.0f, e);
 }
@@ -363,11 +432,27 @@ int rq_qmatmul_dx_mfma(rq_ctx *ctx, const rq_qweight *w, const void *table, cons
     const int64_t n = w->n_out, k = w->k_in;
     _Float16 *x2 = static_cast<_Float16 *>(workspace);
     float *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + (((size_t)m * n * 4 + 255) & ~size_t(255)));
-    if (dy_dtype == RQ_F16)
-        hipLaunchKernelGGL(k_dx_split<true>, dim3((unsigned)m), dim3(256), 0, s, dy, w->scales, x2, xs, n);
-    else
-        hipLaunchKernelGGL(k_dx_split<false>, dim3((unsigned)m), dim3(256), 0, s, dy, w->scales, x2, xs, n);
-    RQ_LAUNCH_CHECK();
+    {
+        const bool vec = aligned(dy, 16) && aligned(w->scales, 16);
+        const int64_t per = cdiv(n / 8, 256);  // 8-value pieces per thread
+        auto go = [&](auto f16, auto v, auto ni) {
+            hipLaunchKernelGGL((k_dx_split<decltype(f16)::value, decltype(v)::value, decltype(ni)::value>),
+                               dim3((unsigned)m), dim3(256), 0, s, dy, w->scales, x2, xs, n);
+        };
+        auto by_ni = [&](auto f16, auto v) {
+            if (per <= 1) go(f16, v, std::integral_constant<int, 1>{});
+            else if (per <= 2) go(f16, v, std::integral_constant<int, 2>{});
+            else if (per <= 4) go(f16, v, std::integral_constant<int, 4>{});
+            else go(f16, v, std::integral_constant<int, 0>{});
+        };
+        auto by_vec = [&](auto f16) {
+            if (vec) by_ni(f16, std::true_type{});
+            else by_ni(f16, std::false_type{});
+        };
+        if (dy_dtype == RQ_F16) by_vec(std::true_type{});
+        else by_vec(std::false_type{});
+        RQ_LAUNCH_CHECK();
+    }
     // the transposed problem: k_in rows of 2 n_out codes, unit scales
     const uint8_t *qt = static_cast<const uint8_t *>(table);
     const rq_qweight wt{qt, reinterpret_cast<const float *>(qt + dx_codes_bytes(*w)), nullptr, k, 2 * n,

@@ -43,39 +43,57 @@ __device__ __forceinline__ float dpp(float v) {
 
 // RQ_LORA_TREE's x . A: block (g, s) takes rows g RM .. g RM + RM - 1 of x
 // and k slice s (TH J values of k); thread tt multiplies k = s TH J + j TH + tt
-// for j < J, its RM RK products accumulated over j in one fma chain each;
-// the block's TH partials of every (row, r) are then summed in a fixed order
-// (through LDS: P = TH / (RM RK) lanes per value each add every P-th
-// partial, then DPP steps over those P lanes) and the slice's sum goes to
-// part[(row KS + s) rank + r].  Rows past m recompute row m - 1 and write
-// nothing; r past rank multiplies zeros.
-template <int RM, int RK, bool F16>
+// for j < J, its RM RK products accumulated over j in one fma chain each
+// (every j's loads issued before the first fma); the block's TH partials of
+// every (row, r) are then summed in a fixed order (through LDS: P = TH /
+// (RM RK) lanes per value each add every P-th partial, then DPP steps over
+// those P lanes) and the slice's sum goes to part[(row KS + s) rank + r].
+// VA (rank % 4 == 0, A 16-byte aligned): a k's rank values as 16-byte loads.
+// Rows past m recompute row m - 1 and write nothing; r past rank multiplies
+// zeros.
+template <int RM, int RK, bool F16, int J, bool VA>
 __global__ __launch_bounds__(TH) void k_lora_xa(const void *__restrict__ xv, const float *__restrict__ a,
-                                                float *__restrict__ part, int64_t m, int64_t K, int rank, int KS,
-                                                int J) {
+                                                float *__restrict__ part, int64_t m, int64_t K, int rank, int KS) {
     constexpr int V = RM * RK, P = TH / V;
     static_assert(TH % V == 0 && (P == 4 || P == 16), "4 or 16 lanes per value");
     __shared__ float red[V][TH + 1];
     const int tt = threadIdx.x, s = blockIdx.y;
     const int64_t i0 = (int64_t)blockIdx.x * RM, k0 = (int64_t)s * TH * J;
+    float av[J][RK], xk[J][RM];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int64_t k = k0 + (int64_t)j * TH + tt;
+        const bool live = k < K;
+        if constexpr (VA) {
+            const float4 *ar = reinterpret_cast<const float4 *>(a + (live ? k : 0) * rank);
+#pragma unroll
+            for (int r4 = 0; r4 < RK / 4; ++r4) {
+                const float4 v = 4 * r4 < rank ? ar[r4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                av[j][4 * r4] = v.x;
+                av[j][4 * r4 + 1] = v.y;
+                av[j][4 * r4 + 2] = v.z;
+                av[j][4 * r4 + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RK; ++r) av[j][r] = r < rank ? a[(live ? k : 0) * rank + r] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < RM; ++i) {
+            const int64_t row = i0 + i < m ? i0 + i : m - 1, o = row * K + (live ? k : 0);
+            const float x = F16 ? (float)static_cast<const _Float16 *>(xv)[o] : static_cast<const float *>(xv)[o];
+            xk[j][i] = live ? x : 0.0f;
+        }
+    }
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.0f;
-    for (int j = 0; j < J; ++j) {
-        const int64_t k = k0 + (int64_t)j * TH + tt;
-        if (k >= K) break;
-        float av[RK];
 #pragma unroll
-        for (int r = 0; r < RK; ++r) av[r] = r < rank ? a[k * rank + r] : 0.0f;
+    for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int i = 0; i < RM; ++i) {
-            const int64_t row = i0 + i < m ? i0 + i : m - 1;
-            const float xk = F16 ? (float)static_cast<const _Float16 *>(xv)[row * K + k]
-                                 : static_cast<const float *>(xv)[row * K + k];
+        for (int i = 0; i < RM; ++i)
 #pragma unroll
-            for (int r = 0; r < RK; ++r) acc[i * RK + r] = __builtin_fmaf(xk, av[r], acc[i * RK + r]);
-        }
-    }
+            for (int r = 0; r < RK; ++r) acc[i * RK + r] = __builtin_fmaf(xk[j][i], av[j][r], acc[i * RK + r]);
 #pragma unroll
     for (int v = 0; v < V; ++v) red[v][tt] = acc[v];
     __syncthreads();
@@ -135,18 +153,21 @@ __global__ __launch_bounds__(TH) void k_lora_out(const float *main, const float 
 }
 
 // The tree's output pass: as k_lora_out (rank <= RB), with t[i][r] the sum
-// over s < KS of part[(i KS + s) rank + r], s ascending.  Per row the block
-// stages the row's KS rank partials in LDS (loaded coalesced, the next row's
-// requested while this one is summed), thread r < rank adds its column of
-// them, and every thread reads the row's t from LDS.
-constexpr int kTreeParts = 8192;  // KS * rank the output pass stages per row
+// over s < KS of part[(i KS + s) rank + r], s ascending.  Block (x, y) takes
+// rows [y rpb, (y + 1) rpb) in chunks of up to RC rows: the chunk's KS rank
+// partials per row are contiguous, staged in LDS with one coalesced load
+// (the chunk's main values requested with them), summed per (row, r) by the
+// block's threads into LDS, then every thread finishes its column of each
+// row -- two barriers per chunk, not per row.
+constexpr int kTreeParts = 8192;  // partials the output pass stages per chunk
+constexpr int kTreeRows = 8;      // rows per chunk (RC)
 template <bool F16, int RB>
 __global__ __launch_bounds__(TH) void k_lora_out_tree(const float *main, const float *__restrict__ part, int KS,
                                                       const float *__restrict__ b, int rank, void *y, int64_t m,
-                                                      int64_t n) {
-    constexpr int PT = kTreeParts / TH;  // staged partials per thread
+                                                      int64_t n, int64_t rpb, int rc_max) {
+    constexpr int RC = kTreeRows;
     __shared__ float pbuf[kTreeParts];
-    __shared__ float tsh[RB];
+    __shared__ float tsh[RC][RB];
     const int tt = threadIdx.x;
     const int64_t c = (int64_t)blockIdx.x * TH + tt;
     const bool live = c < n;
@@ -154,43 +175,39 @@ __global__ __launch_bounds__(TH) void k_lora_out_tree(const float *main, const f
     float bc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) bc[r] = live ? b[(int64_t)(r < rank ? r : 0) * n + c] : 0.0f;
-    float pre[PT];
-    auto fetch = [&](int64_t i) {
-        const float *pr = part + i * np;
+    const int64_t r_begin = (int64_t)blockIdx.y * rpb, r_end = r_begin + rpb < m ? r_begin + rpb : m;
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += rc_max) {
+        const int rc = (int)(r0 + rc_max < r_end ? rc_max : r_end - r0);
+        float mv[RC];
 #pragma unroll
-        for (int j = 0; j < PT; ++j) {
-            const int e = tt + j * TH;
-            if (e < np) pre[j] = pr[e];
-        }
-    };
-    if (blockIdx.y < m) fetch(blockIdx.y);
-    for (int64_t i = blockIdx.y; i < m; i += gridDim.y) {
-#pragma unroll
-        for (int j = 0; j < PT; ++j) {
-            const int e = tt + j * TH;
-            if (e < np) pbuf[e] = pre[j];
+        for (int j = 0; j < RC; ++j) mv[j] = live && j < rc ? main[(r0 + j) * n + c] : 0.0f;
+        const float *pr = part + r0 * np;
+        for (int e = tt; e < rc * np; e += TH) pbuf[e] = pr[e];
+        __syncthreads();
+        for (int pq = tt; pq < rc * rank; pq += TH) {
+            const int j = pq / rank, r = pq % rank;
+            float tv = pbuf[j * np + r];
+            for (int sl = 1; sl < KS; ++sl) tv += pbuf[j * np + sl * rank + r];
+            tsh[j][r] = tv;
         }
         __syncthreads();
-        if (i + gridDim.y < m) fetch(i + gridDim.y);
-        if (tt < rank) {
-            float tv = pbuf[tt];
-            for (int sl = 1; sl < KS; ++sl) tv += pbuf[sl * rank + tt];
-            tsh[tt] = tv;
-        }
-        __syncthreads();
-        float acc = 0.0f;
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            const float f = __builtin_fmaf(tsh[r < rank ? r : 0], bc[r], acc);
-            acc = r < rank ? f : acc;
+        for (int j = 0; j < RC; ++j) {
+            if (j >= rc) break;
+            float acc = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const float f = __builtin_fmaf(tsh[j][r < rank ? r : 0], bc[r], acc);
+                acc = r < rank ? f : acc;
+            }
+            if (live) {
+                const int64_t o = (r0 + j) * n + c;
+                const float v = mv[j] + acc;
+                if constexpr (F16) static_cast<_Float16 *>(y)[o] = (_Float16)v;
+                else static_cast<float *>(y)[o] = v;
+            }
         }
-        if (live) {
-            const int64_t o = i * n + c;
-            const float v = main[o] + acc;
-            if constexpr (F16) static_cast<_Float16 *>(y)[o] = (_Float16)v;
-            else static_cast<float *>(y)[o] = v;
-        }
-        __syncthreads();  // pbuf and tsh are rewritten for the next row
+        __syncthreads();  // pbuf and tsh are rewritten for the next chunk
     }
 }
 
@@ -221,21 +238,34 @@ int launch_lora_xa(const void *x, rq_dtype xt, const float *a, float *part, int6
                    int num_cus, hipStream_t s, int *ks_out) {
     const bool rows4 = rank <= 16 && m > 1;  // 4 rows x 16 ranks per block, else 1 row x 16 or 64
     const int64_t G = cdiv(m, rows4 ? 4 : 1), S1 = std::max<int64_t>(1, cdiv(K, kSlice));
-    // the fewest k per thread that still gives ~2 blocks per CU
+    // the most k per thread (all loaded before the fmas; capped so the
+    // registers hold them) that still gives ~2 blocks per CU
+    const int jmax = rank > 16 ? 2 : (rows4 ? 4 : 8);
     int J = 1;
-    while (J < 8 && G * cdiv(S1, 2 * J) >= 2 * num_cus) J *= 2;
+    while (J < jmax && G * cdiv(S1, 2 * J) >= 2 * num_cus) J *= 2;
     const int64_t KS = std::max<int64_t>(1, cdiv(K, kSlice * J));
     if (G > 0x7fffffff || KS > 65535) return fail(RQ_ERR_SHAPE, "adapter product too large for the tree");
     const dim3 grid((unsigned)G, (unsigned)KS);
-    const bool f16 = xt == RQ_F16;
-    auto go = [&](auto rm, auto rk) {
-        constexpr int RM = decltype(rm)::value, RK = decltype(rk)::value;
-        if (f16) hipLaunchKernelGGL((k_lora_xa<RM, RK, true>), grid, dim3(TH), 0, s, x, a, part, m, K, (int)rank, (int)KS, J);
-        else hipLaunchKernelGGL((k_lora_xa<RM, RK, false>), grid, dim3(TH), 0, s, x, a, part, m, K, (int)rank, (int)KS, J);
+    const bool f16 = xt == RQ_F16, va = rank % 4 == 0 && aligned(a, 16);
+    auto go = [&](auto rm, auto rk, auto jj, auto vv) {
+        constexpr int RM = decltype(rm)::value, RK = decltype(rk)::value, JJ = decltype(jj)::value;
+        constexpr bool VA = decltype(vv)::value;
+        if (f16) hipLaunchKernelGGL((k_lora_xa<RM, RK, true, JJ, VA>), grid, dim3(TH), 0, s, x, a, part, m, K, (int)rank, (int)KS);
+        else hipLaunchKernelGGL((k_lora_xa<RM, RK, false, JJ, VA>), grid, dim3(TH), 0, s, x, a, part, m, K, (int)rank, (int)KS);
     };
-    if (rows4) go(std::integral_constant<int, 4>{}, std::integral_constant<int, 16>{});
-    else if (rank <= 16) go(std::integral_constant<int, 1>{}, std::integral_constant<int, 16>{});
-    else go(std::integral_constant<int, 1>{}, std::integral_constant<int, 64>{});
+    auto by_va = [&](auto rm, auto rk, auto jj) {
+        if (va) go(rm, rk, jj, std::true_type{});
+        else go(rm, rk, jj, std::false_type{});
+    };
+    auto by_j = [&](auto rm, auto rk) {
+        if (J == 1) by_va(rm, rk, std::integral_constant<int, 1>{});
+        else if (J == 2) by_va(rm, rk, std::integral_constant<int, 2>{});
+        else if (J == 4) by_va(rm, rk, std::integral_constant<int, 4>{});
+        else by_va(rm, rk, std::integral_constant<int, 8>{});
+    };
+    if (rows4) by_j(std::integral_constant<int, 4>{}, std::integral_constant<int, 16>{});
+    else if (rank <= 16) by_j(std::integral_constant<int, 1>{}, std::integral_constant<int, 16>{});
+    else by_j(std::integral_constant<int, 1>{}, std::integral_constant<int, 64>{});
     RQ_LAUNCH_CHECK();
     *ks_out = (int)KS;
     return RQ_OK;
@@ -313,8 +343,10 @@ int lora_run(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, 
         constexpr int R = decltype(rb)::value;
         if constexpr (R > 0) {
             if (tree) {
+                const int64_t rpb = cdiv(m, (int64_t)grid.y);
+                const int rc = (int)std::min<int64_t>(kTreeRows, kTreeParts / ((int64_t)KS * rank));
                 hipLaunchKernelGGL((k_lora_out_tree<F, R>), grid, dim3(TH), 0, s, mainv, tv, KS, lora_b, (int)rank, y,
-                                   m, N);
+                                   m, N, rpb, rc);
                 return;
             }
         }
