@@ -48,14 +48,16 @@ def sources() -> list[Path]:
 # all under the same flag:
 #  * epilogues: per-feature scale and per-token power-of-two factor times O(1)
 #    sums; the RoPE rotation of q/k (cos, sin in [-1, 1]); silu(g) * u, whose
-#    results below 2^-126 would round to zero in the fp16 h anyway;
+#    results below 2^-126 would round to zero in the fp16 h anyway; the
+#    matrix-core input gradient's rows (backward.hip), sums of values scaled
+#    to [2^14, 2^15) times their row's 2^e: only results below 2^-126, far
+#    under the row's own resolution, flush;
 #  * k_affine_prep: b - 1024 s per group (a group whose s or b is an f32
 #    denormal dequantizes to 0 instead of ~1e-38);
 #  * k_cast_f16_rows: the row maximum and the x * 2^-e scaling.  An f32
 #    denormal element reads as 0; where the row maximum is normal such an
 #    element is below the fp16 result's resolution (2^-24 of the maximum) in
 #    any case, so only rows made entirely of denormals change (to zero).
-FILE_FLAGS = {"gemm.hip": ["-fgpu-flush-denormals-to-zero"]}
 FILE_FLAGS = {"gemm.hip": ["-fgpu-flush-denormals-to-zero"]}
 
 
