@@ -760,20 +760,24 @@ def vendor_gemm(reps: int = 5) -> list:
     return out
 
 
-def decode_gemv_extra(ctx, use_graph: bool = True) -> dict:
+GEMV_SHAPES = ((4, 4096, 4096, False, False), (16, 4096, 4096, False, False),
+               (1, 11008, 4096, False, False), (8, 11008, 4096, False, False),
+               (1, 4096, 11008, False, False), (8, 4096, 11008, False, False),
+               (1, 4096, 4096, True, False), (4, 4096, 4096, True, False),
+               (16, 4096, 4096, True, False), (1, 4096, 4096, False, True),
+               (4, 4096, 4096, False, True), (16, 4096, 4096, False, True))
+
+
+def decode_gemv_extra(ctx, use_graph: bool = True, shapes=GEMV_SHAPES, reps: int = 20) -> dict:
     """configs[1] at M = 4, 16 and the SwiGLU-shaped GEMVs at M = 1, 8, each
-    over enough rotating weight copies to stay out of the Infinity Cache."""
+    over enough rotating weight copies to stay out of the Infinity Cache
+    (`reps` timed rotations over the copies)."""
     extra = {}
-    for m, n, k, aff, xf in ((4, 4096, 4096, False, False), (16, 4096, 4096, False, False),
-                             (1, 11008, 4096, False, False), (8, 11008, 4096, False, False),
-                             (1, 4096, 11008, False, False), (8, 4096, 11008, False, False),
-                             (1, 4096, 4096, True, False), (4, 4096, 4096, True, False),
-                             (16, 4096, 4096, True, False), (1, 4096, 4096, False, True),
-                             (4, 4096, 4096, False, True), (16, 4096, 4096, False, True)):
+    for m, n, k, aff, xf in shapes:
         copies = max(2, min(COPIES, (1200 << 20) // (n * k)))
         w2 = GemvWorkload(ctx, m, n, k, copies=copies, affine=aff, x_f32=xf)
-        wms, _ = time_steps(ctx, w2, 20 * copies, 2 * copies, use_graph=use_graph)
-        kms = wms / (20 * copies)
+        wms, _ = time_steps(ctx, w2, reps * copies, 2 * copies, use_graph=use_graph)
+        kms = wms / (reps * copies)
         key = f"m{m}_{n}x{k}" + ("_affine" if aff else "") + ("_x_f32" if xf else "")
         extra[key] = {"gbs": round(w2.bytes / (kms * 1e-3) / 1e9, 1), "us_per_launch": round(kms * 1e3, 2),
                       "frac_hbm": round(w2.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": w2.bytes}
@@ -798,8 +802,8 @@ def main() -> int:
                     help="launch every GEMV/prefill/SwiGLU step directly, no HIP graph (for tracers that do not "
                          "follow graph launches; the decode loop has --decode-eager)")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only (for profiling runs)")
-    ap.add_argument("--only", choices=["gemv", "prefill", "prefill_affine", "swiglu", "decode", "decode_probe",
-                                       "floor", "vendor", "ops"],
+    ap.add_argument("--only", choices=["gemv", "gemv_skinny", "prefill", "prefill_affine", "swiglu", "decode",
+                                       "decode_probe", "floor", "vendor", "ops"],
                     help="run one extra workload alone, no headline (for profiling runs)")
     ap.add_argument("--prefill-operands", choices=["random", "zero-activations", "zero-weights"], default="random",
                     help="with --only prefill: zero one operand (same kernel, fewer switching bits) to measure "
@@ -825,6 +829,8 @@ def main() -> int:
         out = {"only": args.only}
         if args.only == "gemv":
             out["decode_gemv"] = decode_gemv_extra(ctx, use_graph=not args.no_graph)
+        elif args.only == "gemv_skinny":  # counter passes: M = 4 and 16 at 4096^2, two rotations each
+            out["decode_gemv"] = decode_gemv_extra(ctx, use_graph=not args.no_graph, shapes=GEMV_SHAPES[:2], reps=2)
         elif args.only == "floor":
             out["floor"] = floor_probe(ctx, GemvWorkload(ctx, 1, 4096, 4096), args.steps, use_graph=not args.no_graph)
         elif args.only == "prefill":
