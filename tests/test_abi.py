@@ -118,3 +118,34 @@ def test_integration_binding_lists_every_entry_point():
     block = block[:block.index("\n}\n")]
     bound = set(re.findall(r"pub fn (rq_[a-z0-9_]+)\s*\(", block))
     assert bound == set(_lib.header_symbols()), bound ^ set(_lib.header_symbols())
+
+
+def test_workspace_and_table_sizes_without_device():
+    """The size queries of the tree LoRA and the matrix-core input gradient are
+    host arithmetic: the documented formulas, 0 for what is not served."""
+    lib = _lib.lib()
+    F16, F32, TREE = _lib.RQ_F16, _lib.RQ_F32, _lib.RQ_LORA_TREE
+    m, k, n, rank = 3, 1000, 512, 16
+    chain = lib.rq_qmatmul_lora_workspace(m, k, n, rank, F16, F16)
+    assert lib.rq_qmatmul_lora_ex_workspace(m, k, n, rank, F16, F16, 0) == chain
+    assert chain == (m * k + m * rank + m * n) * 4 + 3 * 256  # x f32 copy, t, the f32 product
+    # tree: m * rank partials for each of ceil(k / 256) slices, then the f32 product
+    assert lib.rq_qmatmul_lora_ex_workspace(m, k, n, rank, F16, F16, TREE) == (m * rank * 4 + m * n) * 4 + 3 * 256
+    assert lib.rq_qmatmul_lora_ex_workspace(m, k, n, rank, F32, F32, TREE) == m * rank * 4 * 4 + 3 * 256
+    # past rank 64 the tree flag keeps the chain's workspace
+    assert lib.rq_qmatmul_lora_ex_workspace(m, k, n, 70, F16, F16, TREE) == \
+        lib.rq_qmatmul_lora_workspace(m, k, n, 70, F16, F16)
+    assert lib.rq_qmatmul_lora_ex_workspace(-1, k, n, rank, F16, F16, TREE) == 0
+    # the input gradient: fp16 halves of dY (2 m n values) then m row factors
+    assert lib.rq_qmatmul_dx_mfma_workspace(5, 96) == ((5 * 96 * 4 + 255) // 256) * 256 + 5 * 4
+    assert lib.rq_qmatmul_dx_mfma_workspace(-1, 96) == 0
+
+    def desc(fmt, n_out, k_in, codes=4096):
+        return _lib.rq_qweight(codes, 4096, None, n_out, k_in, fmt, 64 if fmt else 0, None)
+
+    w = desc(_lib.RQ_Q_ROWWISE_I8, 96, 48)
+    assert lib.rq_qweight_dx_table_bytes(ctypes.byref(w)) == ((2 * 96 * 48 + 255) // 256) * 256 + 48 * 4
+    for bad in (desc(_lib.RQ_Q_AFFINE_U8, 96, 64), desc(_lib.RQ_Q_ROWWISE_I8, 48, 64),
+                desc(_lib.RQ_Q_ROWWISE_I8, 96, 40), desc(_lib.RQ_Q_ROWWISE_I8, 96, 48, codes=4100)):
+        assert lib.rq_qweight_dx_table_bytes(ctypes.byref(bad)) == 0
+    assert lib.rq_qweight_dx_table_bytes(None) == 0
