@@ -243,7 +243,8 @@ int rq_qmatmul_lora(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_
  * adapter at decode sizes without its latency).  flags 0: exactly
  * rq_qmatmul_lora.  RQ_LORA_TREE (adapters of rank 1..64): X.A as a
  * reduction tree -- slices of 256 k, a fixed-order sum inside each slice, the
- * slices added in order -- deterministic and within f32 rounding of the
+ * slices added in order -- deterministic on a given device (the slice
+ * width follows the compute-unit count) and within f32 rounding of the
  * exact product, but not the reference's bit pattern; wider adapters keep
  * the chain.  The k_in-step fma chain per output that reproduces the
  * reference's bits is latency-bound (~16 us at k_in = 4096, whatever m).
