@@ -12,6 +12,13 @@
  * `device.poll(Wait)` inside `UnifiedTensor::to_vec`, lib.rs:215-240).
  * A context is used from one host thread at a time (the reference's Tensor is
  * RefCell-based and single-threaded, rusty-autograd/src/lib.rs:11-17).
+ * Degenerate sizes are valid for the dequantizers and the products
+ * (rq_qmatmul, rq_mlp_swiglu and its no-alloc variant, rq_qmatmul_lora and
+ * _ex, rq_qmatmul_dx): a call with no tokens or no output elements writes
+ * nothing; an empty reduction (k_in = 0, or a SwiGLU MLP without intermediate
+ * features) writes zeros; a pointer to an operand, adapter or workspace that
+ * holds no element may be NULL.  Entry points with stated shape limits (the
+ * matrix-core input gradient) keep them.
  */
 #ifndef RUSTY_HIP_H
 #define RUSTY_HIP_H

@@ -530,6 +530,9 @@ int rq::swiglu_run(rq_ctx *ctx, const rq_qweight &gate, const rq_qweight &up, co
                    rq_dtype x_dtype, void *h, void *y, rq_dtype y_dtype, int64_t m, const GemmWorkspace &ws,
                    hipStream_t s) {
     const int64_t I = gate.n_out;
+    // no intermediate features: h is empty and the down projection's
+    // reduction too (y = 0)
+    if (I == 0) return qmatmul_dispatch(ctx, down, h, RQ_F16, y, y_dtype, m, ws, s);
     int st = RQ_ERR_UNSUPPORTED;
     if (m <= 2) st = launch_swiglu_decode(gate, up, x, x_dtype, h, (int)m, s);
     if (st == RQ_ERR_UNSUPPORTED && m <= 16) st = launch_swiglu_mfma(gate, up, x, x_dtype, h, (int)m, s);
@@ -576,7 +579,8 @@ int rq_mlp_swiglu(rq_ctx *ctx, const rq_qweight *gate, const rq_qweight *up, con
     RQ_ENTER(ctx);
     int st = swiglu_check(gate, up, down, x_dtype, y_dtype, m);
     if (st != RQ_OK || m == 0 || gate->k_in == 0) return st;
-    if (!y || !h || !x) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation or workspace pointer");
+    // (no intermediate features: h holds nothing and may be null)
+    if (!y || (gate->n_out > 0 && !h) || !x) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation or workspace pointer");
     hipStream_t s = pick(ctx, stream);
     return swiglu_run(ctx, *gate, *up, *down, x, x_dtype, h, y, y_dtype, m, gemm_workspace(ctx, s), s);
 }

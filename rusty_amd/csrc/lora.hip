@@ -289,9 +289,10 @@ int lora_run(rq_ctx *ctx, const rq_qweight *w, const void *x, rq_dtype x_dtype, 
     if (rank > 0x7fffffff || cdiv(N, TH) > 0x7fffffff) return fail(RQ_ERR_SHAPE, "adapter rank or n_out too large");
     if (m == 0 || N == 0) return RQ_OK;
     if (!y || (K > 0 && !x)) return fail(RQ_ERR_INVALID_ARGUMENT, "null activation pointer");
-    if (rank > 0 && (!lora_a || !lora_b)) return fail(RQ_ERR_INVALID_ARGUMENT, "null adapter pointer");
+    // (an empty reduction, k_in = 0, gives A no elements: it may be null)
+    if (rank > 0 && ((K > 0 && !lora_a) || !lora_b)) return fail(RQ_ERR_INVALID_ARGUMENT, "null adapter pointer");
     const size_t need = lora_workspace(m, K, N, rank, x_dtype, y_dtype, flags);
-    if (!workspace || workspace_bytes < need)
+    if ((need > 0 && !workspace) || workspace_bytes < need)
         return fail(RQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
     hipStream_t s = pick(ctx, stream);
     // carve the workspace: chain [x f32][t][main f32], tree [partials][main f32]

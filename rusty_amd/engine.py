@@ -404,7 +404,7 @@ class ComputeEngine:
         """``MLP::forward`` (rusty-graph/src/lib.rs:317-323):
         ``out = down(silu(x . gate^T) * (x . up^T))``.  ``h`` is the fp16
         workspace (2 * m * I values); returned, its first m*I hold silu(g)*u."""
-        m = x.numel // gate.k_in
+        m = x.numel // gate.k_in if gate.k_in else out.shape[0]
         if h is None:
             h = UnifiedTensor.empty(ctx, [2, m, gate.n_out], DType.FP16)
         if h.dtype is not DType.FP16 or h.numel < 2 * m * gate.n_out:
