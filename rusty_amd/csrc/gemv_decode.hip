@@ -615,15 +615,22 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //     norm weight (6 B per element) are read by every block, so more rows per
 //     block (qkv 3072x2048 + norm: 3.98 -> 3.59 us);
 //   * two or more chunks per thread (k_in > 4096): 4 (2048x5632: 4.26 -> 4.17 us);
+//   * f32 activations, row groups of 256 threads: every block reads the whole
+//     f32 row (4 B per element, twice the fp16 row), so 8 rows while that
+//     leaves >= 1024 blocks (>= 512 past k_in = 4096), else 4 while >= 1024,
+//     else 2 (us for 2 / 4 / 8 rows: 4096x4096 5.76 / 5.23 / 5.56, affine
+//     6.18 / 5.60 / 5.60, 11008x4096 11.1 / 10.15 / 10.05, 4096x11008 - /
+//     11.55 / 10.6, 2048x2048 3.25 / 3.40 / 3.90);
 //   * otherwise 2.
 //  m = 2..4: 4 (SwiGLU: 2 pairs).
 //   * attention-combine prologue: 4 (each block re-reads the partials, so
 //     fewer, larger blocks).
 // fmt: 0 = per-row int8, 1 = affine u8; swi selects the SwiGLU gate/up
 // pass; norm (m = 1) the fused RMSNorm prologue; sa (m = 1) the attention
-// combine of sa partials per head; xf (m <= 2, no norm / sa) f32 activations.
+// combine of sa partials per head; xf (m <= 2, no norm / sa) f32 activations:
+// 0 for fp16, else the rows per block of the m = 1 f32 row (2, 4 or 8).
 template <int M, int CPT, int TPR, int FMT>
-Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
+Decode pick_fmt(bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
     if constexpr (M == 1) {
         constexpr int RN = TPR <= 128 ? 6 : 2;   // fused norm
         constexpr int RSN = TPR <= 128 ? 4 : 2;  // SwiGLU pairs with the fused norm
@@ -642,7 +649,16 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
             return xf ? inst<1, CPT, TPR, 8, FMT, false, false, 0, true>() : inst<1, CPT, TPR, 8, FMT, false, false>();
         }
         if (norm) return inst<1, CPT, TPR, RN, FMT, false, true>();
-        return xf ? inst<1, CPT, TPR, RP, FMT, false, false, 0, true>() : inst<1, CPT, TPR, RP, FMT, false, false>();
+        if (xf) {
+            // f32 row: xf rows per block where the row group is the whole block
+            if constexpr (TPR == 256) {
+                if (xf == 8) return inst<1, CPT, TPR, 8, FMT, false, false, 0, true>();
+                if (xf == 4) return inst<1, CPT, TPR, 4, FMT, false, false, 0, true>();
+                return inst<1, CPT, TPR, 2, FMT, false, false, 0, true>();
+            }
+            return inst<1, CPT, TPR, RP, FMT, false, false, 0, true>();
+        }
+        return inst<1, CPT, TPR, RP, FMT, false, false>();
     } else if constexpr (M == 2) {
         (void)norm;
         (void)tall;
@@ -662,13 +678,13 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
 }
 
 template <int M, int CPT, int TPR>
-Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
+Decode pick_swi(int fmt, bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
     return fmt == 0 ? pick_fmt<M, CPT, TPR, 0>(swi, norm, tall, sa, xf, rope)
                     : pick_fmt<M, CPT, TPR, 1>(swi, norm, tall, sa, xf, rope);
 }
 
 template <int M, int CPT>
-Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
+Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
     switch (tpr) {
     case 64: return pick_swi<M, CPT, 64>(fmt, swi, norm, tall, sa, xf, rope);
     case 128: return pick_swi<M, CPT, 128>(fmt, swi, norm, tall, sa, xf, rope);
@@ -677,7 +693,7 @@ Decode pick_tpr(int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool x
 }
 
 template <int M>
-Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa, bool xf, bool rope) {
+Decode pick_cpt(int cpt, int tpr, int fmt, bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
     switch (cpt) {
     case 1: return pick_tpr<M, 1>(tpr, fmt, swi, norm, tall, sa, xf, rope);
     case 2: return pick_tpr<M, 2>(tpr, fmt, swi, norm, tall, sa, xf, rope);
@@ -698,8 +714,9 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
     const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
     const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
-    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall && !rope, sa, xf, rope)
-                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xf, false)
+    const int xr = !xf ? 0 : (N / 8 >= 1024 || (K > 4096 && N / 8 >= 512)) ? 8 : (N / 4 >= 1024 ? 4 : 2);
+    const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall && !rope, sa, xr, rope)
+                             : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xr, false)
                                        : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0, false, false);
     *rows = d.r * (DT / tpr);
     return d;

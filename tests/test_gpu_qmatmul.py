@@ -210,7 +210,8 @@ def test_f32_activations_past_fp16_range(ctx, engine, m, fmt):
                                        (5, 333, 4096, 0), (1, 11008, 4096, 0), (1, 4096, 11008, 0),
                                        (1, 4096, 4096, 1), (2, 1000, 2048, 1), (3, 1000, 2048, 1),
                                        (4, 4096, 4096, 1), (8, 1024, 1024, 1), (16, 4096, 4096, 1),
-                                       (11, 333, 4096, 1)])
+                                       (11, 333, 4096, 1), (1, 11004, 4096, 0), (1, 4100, 8192, 1),
+                                       (1, 4098, 4096, 0)])
 def test_f32_activations_decode_kernels(ctx, engine, m, n, k, fmt):
     g = synth.rng(900 + m + n + fmt)
     x = synth.activations(g, m, k, dtype=np.float32)
