@@ -615,6 +615,8 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //     norm weight (6 B per element) are read by every block, so more rows per
 //     block (qkv 3072x2048 + norm: 3.98 -> 3.59 us);
 //   * two or more chunks per thread (k_in > 4096): 4 (2048x5632: 4.26 -> 4.17 us);
+//     affine codes keep 2 (4 measured 4096x4096 5.19 -> 5.14 us, but the 1.1B
+//     decode step's down projection, 2048x5632, 1886 -> 1860 tok/s);
 //   * f32 activations, row groups of 256 threads: every block reads the whole
 //     f32 row (4 B per element, twice the fp16 row), so 8 rows while that
 //     leaves >= 1024 blocks (>= 512 past k_in = 4096), else 4 while >= 1024,
@@ -622,13 +624,14 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //     6.18 / 5.60 / 5.60, 11008x4096 11.1 / 10.15 / 10.05, 4096x11008 - /
 //     11.55 / 10.6, 2048x2048 3.25 / 3.40 / 3.90);
 //   * otherwise 2.
-//  m = 2..4: 4 (SwiGLU: 2 pairs).
+//  m = 2..4: 4 (SwiGLU: 2 pairs); 8 for f32 activations at m = 2 while that
+//  leaves >= 512 blocks (4096x4096 6.94 -> 6.40 us; fp16 stays at 4: 5.30 vs 5.62).
 //   * attention-combine prologue: 4 (each block re-reads the partials, so
 //     fewer, larger blocks).
 // fmt: 0 = per-row int8, 1 = affine u8; swi selects the SwiGLU gate/up
 // pass; norm (m = 1) the fused RMSNorm prologue; sa (m = 1) the attention
 // combine of sa partials per head; xf (m <= 2, no norm / sa) f32 activations:
-// 0 for fp16, else the rows per block of the m = 1 f32 row (2, 4 or 8).
+// 0 for fp16, else the rows per block for f32 rows (m = 1: 2, 4 or 8; m = 2: 4 or 8).
 template <int M, int CPT, int TPR, int FMT>
 Decode pick_fmt(bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
     if constexpr (M == 1) {
@@ -665,6 +668,7 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
         (void)sa;
         (void)rope;
         if (swi) return xf ? inst<2, CPT, TPR, 2, FMT, true, false, 0, true>() : inst<2, CPT, TPR, 2, FMT, true, false>();
+        if (xf == 8) return inst<2, CPT, TPR, 8, FMT, false, false, 0, true>();
         return xf ? inst<2, CPT, TPR, 4, FMT, false, false, 0, true>() : inst<2, CPT, TPR, 4, FMT, false, false>();
     } else {
         (void)norm;
@@ -714,7 +718,9 @@ static Decode plan(const rq_qweight &w, bool swi, bool norm, int m, int sa, bool
     const int mt = m == 1 ? 1 : (m == 2 ? 2 : 4);
     const int fmt = w.format == RQ_Q_AFFINE_U8 ? 1 : 0;
     const bool tall = mt == 1 && !swi && fmt == 0 && N >= 16384;
-    const int xr = !xf ? 0 : (N / 8 >= 1024 || (K > 4096 && N / 8 >= 512)) ? 8 : (N / 4 >= 1024 ? 4 : 2);
+    const int xr = !xf ? 0
+                   : mt == 2 ? (N / 8 >= 512 ? 8 : 4)
+                             : (N / 8 >= 1024 || (K > 4096 && N / 8 >= 512)) ? 8 : (N / 4 >= 1024 ? 4 : 2);
     const Decode d = mt == 1 ? pick_cpt<1>(cpt, tpr, fmt, swi, norm, tall && !rope, sa, xr, rope)
                              : mt == 2 ? pick_cpt<2>(cpt, tpr, fmt, swi, false, false, 0, xr, false)
                                        : pick_cpt<4>(cpt, tpr, fmt, swi, false, false, 0, false, false);

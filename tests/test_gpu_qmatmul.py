@@ -130,13 +130,13 @@ def test_gemv_row_tile_pairs(ctx, engine, m, n, k):
     assert ok, (max_abs, rel)
 
 
-# m = 1-2: the dot2 GEMV; 3-16: the matrix-core GEMV in blocks of 64 rows over k slices
-# (136 rows: three row blocks, the last ragged; k = 11008 is 43 batches of 256, sliced unevenly)
+# m = 1-2: the dot2 GEMV (138 rows: not a multiple of its 4- or 8-row blocks); 3-16: the
+# matrix-core GEMV (nine 16-row tiles, the last ragged; k = 11008 is 43 batches of 256)
 @pytest.mark.parametrize("k", [1024, 4096, 11008])
 @pytest.mark.parametrize("m", [1, 3, 4, 8, 12, 16])
 def test_gemv_affine_reference_format(ctx, engine, m, k):
     g = synth.rng(m + k)
-    u, s, b = synth.affine_weight(g, 136, k)
+    u, s, b = synth.affine_weight(g, 138, k)
     x = synth.activations(g, m, k)
     y = qmm(ctx, engine, QuantizedTensor.affine(ctx, u, s, b), x, np.float16)
     max_abs, rel, ok = f16_tol_check(y, orc.qlinear_truth(u, s, b, x.astype(np.float32), 1))
@@ -211,7 +211,7 @@ def test_f32_activations_past_fp16_range(ctx, engine, m, fmt):
                                        (1, 4096, 4096, 1), (2, 1000, 2048, 1), (3, 1000, 2048, 1),
                                        (4, 4096, 4096, 1), (8, 1024, 1024, 1), (16, 4096, 4096, 1),
                                        (11, 333, 4096, 1), (1, 11004, 4096, 0), (1, 4100, 8192, 1),
-                                       (1, 4098, 4096, 0)])
+                                       (1, 4098, 4096, 0), (2, 4100, 4096, 0), (2, 4100, 4096, 1)])
 def test_f32_activations_decode_kernels(ctx, engine, m, n, k, fmt):
     g = synth.rng(900 + m + n + fmt)
     x = synth.activations(g, m, k, dtype=np.float32)
