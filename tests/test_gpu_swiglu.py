@@ -190,14 +190,16 @@ def test_swiglu_generic_paths(ctx, engine):
     assert ok
 
 
-@pytest.mark.parametrize("m", [1, 2, 8])
-def test_swiglu_f32_activations(ctx, engine, m):
+@pytest.mark.parametrize("m,inter,hidden", [(1, 1408, 2048), (2, 1408, 2048), (8, 1408, 2048), (1, 1410, 4096)])
+def test_swiglu_f32_activations(ctx, engine, m, inter, hidden):
     """f32 activations (the reference's dtype) through the fused gate/up passes
     (the decode kernel for 1-2 tokens, the matrix-core pass for 3-16): each value
-    split into two fp16 terms, so g and u keep f32 accuracy before h is rounded."""
-    g = synth.rng(700 + m)
-    wg, sg, wu, su, wd, sd = weights(g, 1408, 2048)
-    x = synth.activations(g, m, 2048, dtype=np.float32)
+    split into two fp16 terms, so g and u keep f32 accuracy before h is rounded.
+    hidden 4096 at one token: four gate/up pairs per block, 1410 leaving a
+    ragged last block."""
+    g = synth.rng(700 + m + hidden)
+    wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
+    x = synth.activations(g, m, hidden, dtype=np.float32)
     y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float32)
     _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
     assert ok_h, "intermediate h"
