@@ -624,7 +624,7 @@ constexpr Decode inst() { return {&k_gemv_decode<M, CPT, TPR, R, FMT, SWI, NORM,
 //     6.18 / 5.60 / 5.60, 11008x4096 11.1 / 10.15 / 10.05, 4096x11008 - /
 //     11.55 / 10.6, 2048x2048 3.25 / 3.40 / 3.90);
 //   * otherwise 2.
-//  m = 2..4: 4 (SwiGLU: 2 pairs); 8 for f32 activations at m = 2 while that
+//  m = 2..4: 4 (SwiGLU: 2 pairs, 4 at m = 2 and 256 threads); 8 for f32 activations at m = 2 while that
 //  leaves >= 512 blocks (4096x4096 6.94 -> 6.40 us; fp16 stays at 4: 5.30 vs 5.62).
 //   * attention-combine prologue: 4 (each block re-reads the partials, so
 //     fewer, larger blocks).
@@ -670,7 +670,10 @@ Decode pick_fmt(bool swi, bool norm, bool tall, int sa, int xf, bool rope) {
         (void)tall;
         (void)sa;
         (void)rope;
-        if (swi) return xf ? inst<2, CPT, TPR, 2, FMT, true, false, 0, true>() : inst<2, CPT, TPR, 2, FMT, true, false>();
+        // SwiGLU at 256-thread row groups: 4 pairs (11008x4096 MLP, m = 2: fp16
+        // 26.45 -> 25.95 us, f32 activations 34.35 -> 30.1)
+        constexpr int RS2 = TPR == 256 ? 4 : 2;
+        if (swi) return xf ? inst<2, CPT, TPR, RS2, FMT, true, false, 0, true>() : inst<2, CPT, TPR, RS2, FMT, true, false>();
         if (xf == 8) return inst<2, CPT, TPR, 8, FMT, false, false, 0, true>();
         return xf ? inst<2, CPT, TPR, 4, FMT, false, false, 0, true>() : inst<2, CPT, TPR, 4, FMT, false, false>();
     } else {

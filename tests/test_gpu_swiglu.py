@@ -43,12 +43,14 @@ def weights(g, inter, hidden):
     return wg, sg, wu, su, wd, sd
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16])
-def test_swiglu_small(ctx, engine, m):
-    g = synth.rng(300 + m)
-    wg, sg, wu, su, wd, sd = weights(g, 200, 1024)  # 200: ragged for every row-batch size
-    x = synth.activations(g, m, 1024)
-    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd)
+@pytest.mark.parametrize("m,hidden", [(1, 1024), (2, 1024), (3, 1024), (4, 1024), (5, 1024), (8, 1024),
+                                      (12, 1024), (16, 1024), (2, 4096)])
+def test_swiglu_small(ctx, engine, m, hidden):
+    g = synth.rng(300 + m + hidden)
+    wg, sg, wu, su, wd, sd = weights(g, 200, hidden)  # 200: ragged for every row-batch size
+    x = synth.activations(g, m, hidden)
+    # at hidden 4096 these statistics put |y| past the fp16 range: f32 output
+    y, h = run_mlp(ctx, engine, x, wg, sg, wu, su, wd, sd, ydt=np.float16 if hidden <= 1024 else np.float32)
     _, _, ok_h = f16_tol_check(h, h_truth(x, wg, sg, wu, su))
     assert ok_h, "intermediate h"
     truth = orc.swiglu_truth(wg, sg, wu, su, wd, sd, x.astype(np.float32))
@@ -190,13 +192,14 @@ def test_swiglu_generic_paths(ctx, engine):
     assert ok
 
 
-@pytest.mark.parametrize("m,inter,hidden", [(1, 1408, 2048), (2, 1408, 2048), (8, 1408, 2048), (1, 1410, 4096)])
+@pytest.mark.parametrize("m,inter,hidden", [(1, 1408, 2048), (2, 1408, 2048), (8, 1408, 2048), (1, 1410, 4096),
+                                            (2, 1410, 4096)])
 def test_swiglu_f32_activations(ctx, engine, m, inter, hidden):
     """f32 activations (the reference's dtype) through the fused gate/up passes
     (the decode kernel for 1-2 tokens, the matrix-core pass for 3-16): each value
     split into two fp16 terms, so g and u keep f32 accuracy before h is rounded.
-    hidden 4096 at one token: four gate/up pairs per block, 1410 leaving a
-    ragged last block."""
+    hidden 4096 at one or two tokens: four gate/up pairs per block, 1410
+    leaving a ragged last block."""
     g = synth.rng(700 + m + hidden)
     wg, sg, wu, su, wd, sd = weights(g, inter, hidden)
     x = synth.activations(g, m, hidden, dtype=np.float32)
