@@ -1,4 +1,6 @@
-"""Seeded sweep of the fused quantized linear (rq_qmatmul) over random shapes.
+"""Seeded sweeps over random shapes: the fused quantized linear (rq_qmatmul),
+the SwiGLU MLP, and -- bit for bit -- the f32 matmul family and the
+frozen-weight input gradient.  For the fused linear:
 
 Forty cases drawn from one fixed seed: token counts across every dispatch tier
 (the decode GEMVs at 1-2 tokens, the matrix-core GEMV at 3-16, the prefill
@@ -100,3 +102,64 @@ def test_swiglu_random_shapes(ctx, engine, m, inter, hidden, xdt):
     print(f"[sweep mlp m={m} I={inter} H={hidden} x={np.dtype(xdt).name}] max_abs={max_abs:.3e} rel={rel:.3e}",
           flush=True)
     assert ok
+
+
+def _mm_cases(n_cases=16, seed=20261204):
+    g = np.random.default_rng(seed)
+    out = []
+    while len(out) < n_cases:
+        m, k, n = (int(v) for v in g.integers(1, [600, 1500, 900]))
+        if m * k * n <= 30_000_000:
+            out.append((m, k, n))
+    return out
+
+
+@pytest.mark.parametrize("m,k,n", _mm_cases())
+def test_matmul_family_random_shapes_bit_exact(ctx, engine, m, k, n):
+    """matmul / matmul_bt / matmul_at (kernels.wgsl:7-54, 234-252) over random
+    shapes: bit for bit the oracle's k-ascending fused f32 loop."""
+    g = np.random.default_rng(m * 31 + k * 7 + n)
+    a = g.standard_normal((m, k), dtype=np.float32)
+    b = g.standard_normal((k, n), dtype=np.float32)
+
+    def run(op, x, y):
+        out = UnifiedTensor.new(ctx, np.full((m, n), np.nan, np.float32))
+        getattr(engine, op)(ctx, UnifiedTensor.new(ctx, x), UnifiedTensor.new(ctx, y), out)
+        return out.to_vec().view(np.uint32)
+
+    bt, at = np.ascontiguousarray(b.T), np.ascontiguousarray(a.T)
+    assert np.array_equal(run("matmul", a, b), orc.matmul(a, b, fused=True).view(np.uint32))
+    assert np.array_equal(run("matmul_bt", a, bt), orc.matmul_bt(a, bt, fused=True).view(np.uint32))
+    assert np.array_equal(run("matmul_at", at, b), orc.matmul_at(at, b, fused=True).view(np.uint32))
+
+
+def _dx_cases(n_cases=12, seed=20261205):
+    g = np.random.default_rng(seed)
+    out = []
+    while len(out) < n_cases:
+        m, n_out, k_in = (int(v) for v in g.integers(1, [300, 1500, 1500]))
+        if m * n_out * k_in <= 40_000_000:
+            out.append((m, n_out, k_in, int(g.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("m,n_out,k_in,fmt", _dx_cases())
+def test_dx_random_shapes_bit_exact(ctx, engine, m, n_out, k_in, fmt):
+    """The frozen-weight input gradient (MatMulNode::backward's grad_a,
+    rusty-autograd/src/lib.rs:152-158) over random shapes, f32: bit for bit the
+    oracle's fused k-ascending matmul of dY with the dequantized weight."""
+    g = synth.rng(m * 131 + n_out * 17 + k_in + fmt)
+    if fmt == 0:
+        q, s = synth.rowwise_weight(g, n_out, k_in)
+        w, wdeq = QuantizedTensor.rowwise(ctx, q, s), orc.rowwise_dequantize(q, s)
+    else:
+        u, s, b = synth.affine_weight(g, n_out, k_in, group=64)
+        w = QuantizedTensor.affine(ctx, u, s, b, group=64)
+        wdeq = orc.affine_dequantize(u, s, b, group=64)
+    dy = g.standard_normal((m, n_out), dtype=np.float32)
+    dx = UnifiedTensor.new(ctx, np.full((m, k_in), np.nan, np.float32))
+    engine.qmatmul_dx(ctx, UnifiedTensor.new(ctx, dy), w, dx)
+    want = orc.matmul(dy, wdeq.reshape(n_out, k_in), fused=True)
+    got = dx.to_vec()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"{np.count_nonzero(got.view(np.uint32) != want.view(np.uint32))} elements differ"
