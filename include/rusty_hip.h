@@ -331,9 +331,10 @@ int rq_qmatmul_dx_mfma(rq_ctx *ctx, const rq_qweight *w, const void *table, cons
  * with RoPE and a KV cache (:191-283; KVCacheLayer :473-478), RMSNorm
  * (kernels.wgsl:87-102, every row), greedy top_k with k = 1
  * (kernels.wgsl:173-188) and the embedding gather (lib.rs:121-135) on the
- * device.  The reference has no decode loop; this runner defines it: each
- * step is one HIP graph launch, with the position, the token sequence and the
- * KV cache in device memory.  Weights are borrowed (device pointers that must
+ * device.  The reference has no decode loop; this runner defines it: steps
+ * are replayed from captured HIP graphs (four steps per launch, see
+ * rq_llama_decode), with the position, the token sequence and the KV cache
+ * in device memory.  Weights are borrowed (device pointers that must
  * outlive the runner) except q/k/v, which are packed into one [q;k;v] weight
  * owned by the runner at create. */
 typedef struct rq_llama_config {
