@@ -38,7 +38,11 @@ __device__ __forceinline__ uint32_t lds_addr(T *p) {
 // as inline asm so the compiler does not turn its conservative LDS-DMA alias
 // tracking into a full vmcnt(0) wait before every LDS read; every reader of a
 // stage waits with an explicit s_waitcnt vmcnt instead.  M0 carries the LDS
-// base (one wait state before the load, as the ISA requires).
+// base (one wait state before the load, as the ISA requires).  The compiler
+// reserves M0 and warns that the "m0" clobber is not honoured (-Winline-asm):
+// that is safe only while nothing else in these kernels holds a value in M0
+// across a DMA, and in the device assembly of gemm.hip and matmul_f32.hip the
+// only instructions naming M0 are these moves (each directly before its load).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
     const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
